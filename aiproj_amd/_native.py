@@ -1,0 +1,121 @@
+"""ctypes binding of `libkvfp8.so`, the gfx950 HIP kernels behind the reference API.
+
+The library is built in-tree by `aiproj_amd.build` (or `__graft_entry__.build()`).
+There is no fallback: if the library is missing or fails to load, every entry point
+that needs it raises, so a GPU run can never silently take another code path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+LIBRARY_PATH = Path(__file__).resolve().parent / "libkvfp8.so"
+
+# enum kvfp8_dtype in include/kvfp8.h
+F32, F16, BF16, E4M3FN, I32, I64 = 0, 1, 2, 3, 4, 5
+
+TORCH_TO_CODE = {
+    torch.float32: F32,
+    torch.float16: F16,
+    torch.bfloat16: BF16,
+    torch.float8_e4m3fn: E4M3FN,
+    torch.int32: I32,
+    torch.int64: I64,
+}
+
+# Exported symbols and their C signatures (include/kvfp8.h).
+_P = ctypes.c_void_p
+_I32 = ctypes.c_int32
+_I64 = ctypes.c_int64
+_INT = ctypes.c_int
+SIGNATURES = {
+    "kvfp8_quantize_append": (_INT, [_P, _P, _INT, _I64, _I64, _I64, _I64, _P, _INT, _P, _INT,
+                                     _I64, _I32, _I32, _I64, _I32, _P, _P, _P, _P, _P]),
+    "kvfp8_store_append": (_INT, [_P, _P, _INT, _I64, _I64, _I64, _I64, _P, _INT, _P, _INT,
+                                  _I64, _I32, _I32, _I64, _I32, _P, _P, _INT, _P]),
+    "kvfp8_decode_workspace_bytes": (_I64, [_I32, _I32, _I32, _I32, _I64, _I32, _INT]),
+    "kvfp8_paged_decode": (_INT, [_P, _INT, _I64, _I64, _I32, _I32, _I32, _I32, _P, _P, _INT,
+                                  _P, _P, _I64, _I32, _P, _I64, _I64, _P, _INT, _P, _INT,
+                                  ctypes.c_float, _P, _P, _I64, _P]),
+    "kvfp8_timing_enable": (_INT, [_I32]),
+    "kvfp8_timing_read": (_INT, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I64)]),
+    "kvfp8_strerror": (ctypes.c_char_p, [_INT]),
+    "kvfp8_version": (ctypes.c_char_p, []),
+    "kvfp8_host_encode_e4m3fn": (None, [_P, _P, _I64]),
+    "kvfp8_host_quantize_rows": (None, [_P, _I64, _I32, _P, _P]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class NativeLibraryError(RuntimeError):
+    """libkvfp8.so is missing or unusable."""
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library (loaded once). Raises NativeLibraryError if it is absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIBRARY_PATH.exists():
+                raise NativeLibraryError(
+                    f"{LIBRARY_PATH} is not built; run `python -m aiproj_amd.build` "
+                    "(the FP8 KV-cache path has no non-HIP implementation)"
+                )
+            handle = ctypes.CDLL(str(LIBRARY_PATH))
+            for name, (restype, argtypes) in SIGNATURES.items():
+                fn = getattr(handle, name)
+                fn.restype = restype
+                fn.argtypes = argtypes
+            _lib = handle
+    return _lib
+
+
+def strerror(code: int) -> str:
+    return lib().kvfp8_strerror(code).decode()
+
+
+def check(code: int, what: str) -> None:
+    """Map a C-ABI return code to the reference's exception types."""
+    if code == 0:
+        return
+    if code < 0:
+        raise ValueError(f"{what}: {strerror(code)} (code {code})")
+    raise RuntimeError(f"{what}: HIP error {code}: {strerror(code)}")
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return TORCH_TO_CODE[dtype]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {dtype}") from None
+
+
+def ptr(tensor) -> int | None:
+    return None if tensor is None else tensor.data_ptr()
+
+
+def stream_handle(device: torch.device) -> int:
+    """The current HIP stream of `device`, as the raw handle the C ABI takes."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def require_gpu(*tensors, what: str) -> torch.device:
+    """All tensors on one GPU device; the FP8 path has no CPU implementation."""
+    devices = {t.device for t in tensors if t is not None}
+    if len(devices) != 1:
+        raise ValueError(f"{what}: tensors span devices {sorted(map(str, devices))}")
+    device = devices.pop()
+    if device.type != "cuda":
+        raise RuntimeError(
+            f"{what}: tensors are on {device}; the FP8 KV-cache kernels run on the GPU only "
+            "(like the reference, there is no CPU FP8 path)"
+        )
+    return device

@@ -1,0 +1,422 @@
+// Paged decode attention over the (FP8 or plain) paged KV cache, gfx950.
+//
+// Replaces `decode_attention_wrapper` and the Triton split / reduction kernels of
+// reference src/torch_llm/kernals/decode_attention.py:39-550.
+//
+// Launch structure (two kernels, one stream, no host synchronization):
+//   1. a split kernel. Every workgroup first scans context_lengths into an LDS
+//      prefix of per-sequence chunk counts (a chunk is `chunk_tokens` tokens of
+//      one sequence), then its waves grid-stride over the flat work list
+//      (sequence, chunk, head unit). A sequence that fits one chunk is finished
+//      in place; otherwise each chunk leaves a partial softmax state (m, l, acc)
+//      in the workspace.
+//   2. a combine kernel, one wave per (sequence, q head), that merges the
+//      partials of multi-chunk sequences (the reference's reduction kernel,
+//      decode_attention.py:437-550) and writes zeros for empty sequences.
+// Scores are kept in the base-2 domain (q * sm_scale * log2 e, then exp2).
+//
+// The split kernel here is the generic VALU one (every cache dtype, any head
+// size up to 512, any group size; one wave per (sequence, chunk, q head)). The
+// FP8 MFMA kernel in kvfp8_decode_mfma.hip is dispatched when its shape
+// conditions hold.
+#include "kvfp8_decode_common.h"
+#include "kvfp8_decode_mfma.h"
+
+#include <vector>
+
+namespace kvfp8 {
+
+constexpr int kDecodeThreads = 256;
+constexpr int kWavesPerBlock = kDecodeThreads / 64;
+constexpr int kMaxBatch = 8191;          // LDS prefix of (batch + 1) int32 <= 32 KiB
+constexpr int kGenericChunkTokens = 256;
+constexpr int kMaxGrid = 2048;
+
+template <int KVT> struct KvLoad;
+template <> struct KvLoad<KVFP8_E4M3FN> {
+    static __device__ __forceinline__ float at(const void* p, int64_t i) {
+        return decode_e4m3fn(reinterpret_cast<const uint8_t*>(p)[i]);
+    }
+};
+template <int DT> struct KvLoad {
+    static __device__ __forceinline__ float at(const void* p, int64_t i) {
+        return Elem<DT>::load(reinterpret_cast<const typename Elem<DT>::T*>(p)[i]);
+    }
+};
+
+// One wave per (sequence, chunk, q head). Lane = (token tok in 0..15, part in
+// 0..3); a lane covers head dims d = part + 4 i, i < DQ (so D <= 4 DQ).
+template <int KVT, int QT, int DQ>
+__global__ void __launch_bounds__(kDecodeThreads)
+decode_split_generic(DecodeArgs a) {
+    extern __shared__ int32_t prefix[];
+    build_chunk_prefix<kDecodeThreads>(a, prefix);
+
+    const int U = a.num_q_heads;
+    const int64_t total = (int64_t)prefix[a.batch] * U;
+    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const int tok = lane >> 2, part = lane & 3;
+    const int G = a.num_q_heads / a.num_kv_heads;
+    const int D = a.head_dim;
+    const int64_t bs_mask = a.block_size - 1;
+    constexpr bool kQuant = KVT == KVFP8_E4M3FN;
+
+    for (int64_t w = (int64_t)blockIdx.x * kWavesPerBlock + wave; w < total;
+         w += (int64_t)gridDim.x * kWavesPerBlock) {
+        const int32_t chunk = (int32_t)(w / U);
+        const int hq = (int)(w - (int64_t)chunk * U);
+        const int b = find_seq(prefix, a.batch, chunk);
+        const int c = chunk - prefix[b];
+        const int nchunks = prefix[b + 1] - prefix[b];
+        int64_t slot;
+        const int64_t len = seq_tokens(a, b, &slot);
+        const int h = hq / G;
+        const int64_t t0 = (int64_t)c * a.chunk_tokens;
+        const int64_t t1 = min(t0 + (int64_t)a.chunk_tokens, len);
+        const int32_t* table_row = a.block_table + slot * a.bt_width;
+
+        float qv[DQ], acc[DQ];
+#pragma unroll
+        for (int i = 0; i < DQ; ++i) {
+            const int d = part + 4 * i;
+            qv[i] = d < D ? load_q<QT>(a, b, hq, d) * a.score_scale : 0.0f;
+            acc[i] = 0.0f;
+        }
+        float m = kNegInf, l = 0.0f;
+
+        for (int64_t base = t0; base < t1; base += 16) {
+            const int64_t t = base + tok;
+            bool valid = t < t1;
+            int64_t row = 0;
+            if (valid) {
+                const int64_t phys = table_row[t >> a.bs_shift];
+                valid = phys >= 0 && phys < a.num_blocks;
+                row = ((phys << a.bs_shift) + (t & bs_mask)) * a.num_kv_heads + h;
+                row = valid ? row : 0;
+            }
+            float s = 0.0f;
+            if (valid) {
+#pragma unroll
+                for (int i = 0; i < DQ; ++i) {
+                    const int d = part + 4 * i;
+                    if (d < D) s += qv[i] * KvLoad<KVT>::at(a.k_cache, row * D + d);
+                }
+            }
+            s += __shfl_xor(s, 1);
+            s += __shfl_xor(s, 2);
+            float ks = 1.0f, vs = 1.0f;
+            if (kQuant && valid) {
+                ks = a.k_scales[row];
+                vs = a.v_scales[row];
+            }
+            s = valid ? s * ks : kNegInf;
+            float mt = s;
+#pragma unroll
+            for (int off = 4; off < 64; off <<= 1) mt = fmaxf(mt, __shfl_xor(mt, off));
+            const float m_new = fmaxf(m, mt);
+            if (m_new == kNegInf) continue;          // no valid token yet (wave-uniform)
+            const float alpha = exp2f(m - m_new);
+            const float p = valid ? exp2f(s - m_new) : 0.0f;
+            l = l * alpha + p;
+            const float pv = p * vs;
+#pragma unroll
+            for (int i = 0; i < DQ; ++i) {
+                const int d = part + 4 * i;
+                const float v = (valid && d < D) ? KvLoad<KVT>::at(a.v_cache, row * D + d) : 0.0f;
+                acc[i] = acc[i] * alpha + (valid ? pv * v : 0.0f);
+            }
+            m = m_new;
+        }
+
+#pragma unroll
+        for (int off = 4; off < 64; off <<= 1) {
+            l += __shfl_xor(l, off);
+#pragma unroll
+            for (int i = 0; i < DQ; ++i) acc[i] += __shfl_xor(acc[i], off);
+        }
+
+        if (nchunks == 1) {
+            if (tok == 0) {
+                const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+#pragma unroll
+                for (int i = 0; i < DQ; ++i) {
+                    const int d = part + 4 * i;
+                    if (d < D) store_out<QT>(a, b, hq, d, l > 0.0f ? acc[i] * inv : 0.0f);
+                }
+            }
+        } else {
+            const int64_t pi = part_index(a, b, c, hq);
+            if (lane == 0) {
+                a.part_m[pi] = m;
+                a.part_l[pi] = l;
+            }
+            if (tok == 0) {
+#pragma unroll
+                for (int i = 0; i < DQ; ++i) {
+                    const int d = part + 4 * i;
+                    if (d < D) a.part_acc[pi * D + d] = acc[i];
+                }
+            }
+        }
+    }
+}
+
+// Merge of split-K partials, reference decode_attention.py:437-550:
+//   M = max_c m_c; den = sum_c 2^(m_c - M) l_c; num = sum_c 2^(m_c - M) acc_c
+//   out = den > 0 ? num / den : 0
+// One wave per (sequence, q head); sequences with one chunk were written by the
+// split kernel, sequences with none get zeros here.
+template <int QT>
+__global__ void __launch_bounds__(kDecodeThreads)
+decode_combine(DecodeArgs a) {
+    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const int64_t pair = (int64_t)blockIdx.x * kWavesPerBlock + wave;
+    if (pair >= (int64_t)a.batch * a.num_q_heads) return;
+    const int b = (int)(pair / a.num_q_heads);
+    const int hq = (int)(pair - (int64_t)b * a.num_q_heads);
+    int64_t slot;
+    const int n = seq_chunks(seq_tokens(a, b, &slot), a.chunk_tokens);
+    if (n == 1) return;
+    const int D = a.head_dim;
+    if (n == 0) {
+        for (int d = lane; d < D; d += 64) store_out<QT>(a, b, hq, d, 0.0f);
+        return;
+    }
+    float M = kNegInf;
+    for (int c = 0; c < n; ++c) M = fmaxf(M, a.part_m[part_index(a, b, c, hq)]);
+    for (int d = lane; d < D; d += 64) {
+        float num = 0.0f, den = 0.0f;
+        for (int c = 0; c < n; ++c) {
+            const int64_t pi = part_index(a, b, c, hq);
+            const float wgt = M == kNegInf ? 0.0f : exp2f(a.part_m[pi] - M);
+            den += wgt * a.part_l[pi];
+            num += wgt * a.part_acc[pi * D + d];
+        }
+        store_out<QT>(a, b, hq, d, den > 0.0f ? num / den : 0.0f);
+    }
+}
+
+}  // namespace kvfp8
+
+using namespace kvfp8;
+
+namespace {
+
+struct Plan {
+    bool mfma;
+    int32_t chunk_tokens;
+    int32_t max_chunks;
+    int32_t units;      // head units per chunk: q heads (generic) or kv heads (MFMA)
+};
+
+Plan make_plan(int32_t batch, int32_t hq, int32_t hkv, int32_t d, int64_t bt_width, int32_t bs, int kv_dtype) {
+    Plan p;
+    p.mfma = mfma_decode_supported(hq, hkv, d, kv_dtype);
+    p.chunk_tokens = p.mfma ? mfma_chunk_tokens(batch, hkv, bt_width, bs) : kGenericChunkTokens;
+    const int64_t cap = bt_width * bs;
+    p.max_chunks = (int32_t)((cap + p.chunk_tokens - 1) / p.chunk_tokens);
+    p.units = p.mfma ? hkv : hq;
+    return p;
+}
+
+bool pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
+
+int ilog2(int64_t x) {
+    int s = 0;
+    while ((int64_t)1 << s < x) ++s;
+    return s;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+int64_t workspace_for(const Plan& p, int32_t batch, int32_t hq, int32_t d) {
+    const int64_t states = (int64_t)batch * p.max_chunks * hq;
+    return (int64_t)(2 * align256(states * sizeof(float)) + align256(states * d * sizeof(float)));
+}
+
+template <int KVT, int QT>
+hipError_t launch_generic(const DecodeArgs& a, int64_t units_total, hipStream_t s) {
+    const size_t lds = (size_t)(a.batch + 1) * sizeof(int32_t);
+    int64_t blocks = (units_total + kWavesPerBlock - 1) / kWavesPerBlock;
+    blocks = blocks < 1 ? 1 : (blocks > kMaxGrid ? kMaxGrid : blocks);
+    const dim3 grid((unsigned)blocks), block(kDecodeThreads);
+    if (a.head_dim <= 128)
+        hipLaunchKernelGGL((decode_split_generic<KVT, QT, 32>), grid, block, lds, s, a);
+    else if (a.head_dim <= 256)
+        hipLaunchKernelGGL((decode_split_generic<KVT, QT, 64>), grid, block, lds, s, a);
+    else
+        hipLaunchKernelGGL((decode_split_generic<KVT, QT, 128>), grid, block, lds, s, a);
+    return hipGetLastError();
+}
+
+template <int QT>
+hipError_t launch_combine(const DecodeArgs& a, hipStream_t s) {
+    const int64_t pairs = (int64_t)a.batch * a.num_q_heads;
+    const dim3 grid((unsigned)((pairs + kWavesPerBlock - 1) / kWavesPerBlock));
+    hipLaunchKernelGGL((decode_combine<QT>), grid, dim3(kDecodeThreads), 0, s, a);
+    return hipGetLastError();
+}
+
+// Event pairs around split-kernel launches, armed by kvfp8_timing_enable.
+struct SplitTiming {
+    std::vector<hipEvent_t> start, stop;
+    int32_t armed = 0;
+    int32_t used = 0;
+};
+SplitTiming g_timing;
+
+void timing_before(hipStream_t s) {
+    if (g_timing.used < g_timing.armed) hipEventRecord(g_timing.start[g_timing.used], s);
+}
+
+void timing_after(hipStream_t s) {
+    if (g_timing.used < g_timing.armed) hipEventRecord(g_timing.stop[g_timing.used++], s);
+}
+
+template <int QT>
+hipError_t dispatch_kv(const DecodeArgs& a, int kv_dtype, const Plan& p, hipStream_t s) {
+    const int64_t units_total = (int64_t)a.batch * p.max_chunks * p.units;
+    hipError_t err;
+    timing_before(s);
+    if (p.mfma) {
+        err = launch_mfma_decode<QT>(a, units_total, s);
+    } else {
+        switch (kv_dtype) {
+            case KVFP8_E4M3FN: err = launch_generic<KVFP8_E4M3FN, QT>(a, units_total, s); break;
+            case KVFP8_BF16: err = launch_generic<KVFP8_BF16, QT>(a, units_total, s); break;
+            case KVFP8_F16: err = launch_generic<KVFP8_F16, QT>(a, units_total, s); break;
+            default: err = launch_generic<KVFP8_F32, QT>(a, units_total, s); break;
+        }
+    }
+    timing_after(s);
+    if (err != hipSuccess) return err;
+    return launch_combine<QT>(a, s);
+}
+
+}  // namespace
+
+extern "C" int64_t kvfp8_decode_workspace_bytes(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+                                                int32_t head_dim, int64_t bt_width, int32_t block_size,
+                                                int kv_dtype) {
+    if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || bt_width <= 0 ||
+        block_size <= 0)
+        return 0;
+    const Plan p = make_plan(batch, num_q_heads, num_kv_heads, head_dim, bt_width, block_size, kv_dtype);
+    return workspace_for(p, batch, num_q_heads, head_dim);
+}
+
+extern "C" int kvfp8_paged_decode(const void* q, int q_dtype, int64_t q_stride_b, int64_t q_stride_h,
+                                  int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                  const void* k_cache, const void* v_cache, int kv_dtype,
+                                  const float* k_scales, const float* v_scales, int64_t num_blocks,
+                                  int32_t block_size, const int32_t* block_table, int64_t bt_rows,
+                                  int64_t bt_width, const void* slots, int slots_dtype,
+                                  const void* context_lengths, int ctx_dtype, float sm_scale, void* out,
+                                  void* workspace, int64_t workspace_bytes, void* stream) {
+    if (q_dtype != KVFP8_F32 && q_dtype != KVFP8_F16 && q_dtype != KVFP8_BF16) return KVFP8_EDTYPE;
+    if (kv_dtype != KVFP8_E4M3FN && kv_dtype != KVFP8_BF16 && kv_dtype != KVFP8_F16 && kv_dtype != KVFP8_F32)
+        return KVFP8_EDTYPE;
+    if ((slots_dtype != KVFP8_I32 && slots_dtype != KVFP8_I64) || (ctx_dtype != KVFP8_I32 && ctx_dtype != KVFP8_I64))
+        return KVFP8_EDTYPE;
+    if (batch < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || num_blocks <= 0 ||
+        bt_rows <= 0 || bt_width <= 0 || num_q_heads % num_kv_heads != 0 || !pow2(block_size))
+        return KVFP8_ESHAPE;
+    if (batch == 0) return KVFP8_OK;
+    if (batch > kMaxBatch || head_dim > 512) return KVFP8_ELIMIT;
+    if (!q || !k_cache || !v_cache || !block_table || !slots || !context_lengths || !out) return KVFP8_ENULL;
+    if (kv_dtype == KVFP8_E4M3FN && (!k_scales || !v_scales)) return KVFP8_ENULL;
+
+    const Plan p = make_plan(batch, num_q_heads, num_kv_heads, head_dim, bt_width, block_size, kv_dtype);
+    const int64_t need = workspace_for(p, batch, num_q_heads, head_dim);
+    if (!workspace || workspace_bytes < need) return KVFP8_EWORKSPACE;
+
+    const int64_t states = (int64_t)batch * p.max_chunks * num_q_heads;
+    char* ws = reinterpret_cast<char*>(workspace);
+    DecodeArgs a;
+    a.q = q;
+    a.q_stride_b = q_stride_b;
+    a.q_stride_h = q_stride_h;
+    a.batch = batch;
+    a.num_q_heads = num_q_heads;
+    a.num_kv_heads = num_kv_heads;
+    a.head_dim = head_dim;
+    a.k_cache = k_cache;
+    a.v_cache = v_cache;
+    a.k_scales = k_scales;
+    a.v_scales = v_scales;
+    a.num_blocks = num_blocks;
+    a.block_size = block_size;
+    a.bs_shift = ilog2(block_size);
+    a.block_table = block_table;
+    a.bt_rows = bt_rows;
+    a.bt_width = bt_width;
+    a.slots = slots;
+    a.ctx = context_lengths;
+    a.slots64 = slots_dtype == KVFP8_I64;
+    a.ctx64 = ctx_dtype == KVFP8_I64;
+    a.score_scale = sm_scale * kLog2e;
+    a.out = out;
+    a.part_m = reinterpret_cast<float*>(ws);
+    a.part_l = reinterpret_cast<float*>(ws + align256(states * sizeof(float)));
+    a.part_acc = reinterpret_cast<float*>(ws + 2 * align256(states * sizeof(float)));
+    a.chunk_tokens = p.chunk_tokens;
+    a.max_chunks = p.max_chunks;
+
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    hipError_t err;
+    switch (q_dtype) {
+        case KVFP8_F32: err = dispatch_kv<KVFP8_F32>(a, kv_dtype, p, s); break;
+        case KVFP8_F16: err = dispatch_kv<KVFP8_F16>(a, kv_dtype, p, s); break;
+        default: err = dispatch_kv<KVFP8_BF16>(a, kv_dtype, p, s); break;
+    }
+    return (int)err;
+}
+
+extern "C" const char* kvfp8_strerror(int code) {
+    switch (code) {
+        case KVFP8_OK: return "ok";
+        case KVFP8_EDTYPE: return "unsupported dtype";
+        case KVFP8_ESHAPE: return "inconsistent or non-positive sizes";
+        case KVFP8_ESTRIDE: return "unsupported stride or alignment";
+        case KVFP8_ENULL: return "required pointer is NULL";
+        case KVFP8_EWORKSPACE: return "workspace too small";
+        case KVFP8_ELIMIT: return "size beyond what the kernels support";
+        default: return code > 0 ? hipGetErrorString((hipError_t)code) : "unknown error";
+    }
+}
+
+extern "C" int kvfp8_timing_enable(int32_t max_launches) {
+    g_timing.armed = 0;
+    g_timing.used = 0;
+    if (max_launches <= 0) return KVFP8_OK;
+    while ((int32_t)g_timing.start.size() < max_launches) {
+        hipEvent_t a, b;
+        hipError_t err = hipEventCreate(&a);
+        if (err != hipSuccess) return (int)err;
+        err = hipEventCreate(&b);
+        if (err != hipSuccess) return (int)err;
+        g_timing.start.push_back(a);
+        g_timing.stop.push_back(b);
+    }
+    g_timing.armed = max_launches;
+    return KVFP8_OK;
+}
+
+extern "C" int kvfp8_timing_read(double* total_ms, int64_t* launches) {
+    double sum = 0.0;
+    for (int32_t i = 0; i < g_timing.used; ++i) {
+        hipError_t err = hipEventSynchronize(g_timing.stop[i]);
+        if (err != hipSuccess) return (int)err;
+        float ms = 0.0f;
+        err = hipEventElapsedTime(&ms, g_timing.start[i], g_timing.stop[i]);
+        if (err != hipSuccess) return (int)err;
+        sum += ms;
+    }
+    if (total_ms) *total_ms = sum;
+    if (launches) *launches = g_timing.used;
+    g_timing.armed = 0;
+    g_timing.used = 0;
+    return KVFP8_OK;
+}
+
+extern "C" const char* kvfp8_version(void) { return "kvfp8 1 gfx950"; }

@@ -1,0 +1,307 @@
+#!/usr/bin/env python
+"""Benchmark of the FP8 paged KV-cache decode step on one MI355X.
+
+A step is one pass of the hot path over one batch: quantize-and-scatter the new
+K/V token of every sequence into the FP8 paged cache, then paged decode attention
+of every sequence over its whole context (reference call site
+`src/torch_llm/model/attention.py:86-99`). Inputs are synthetic and resident in HBM
+before timing starts. Independent cache pools are rotated step to step so their
+total exceeds twice the 256 MB Infinity Cache: every step reads its KV from HBM.
+
+Default workload ("north"): B=32, 32 q / 8 KV heads, D=128, page 16, every
+context 4096 tokens, e4m3fn cache, bf16 q (the metric's "B=32 4k ctx"). The
+cfg2 draw (contexts ~ U[512, 4096]) is measured too and reported as `secondary`.
+
+Prints one JSON line on stdout; progress goes to stderr.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "FP8 paged decode-attn HBM GB/s (% of peak) + KV tokens/s, B=32 4k ctx"
+PEAK_HBM_GBS = 8000.0
+MALL_BYTES = 256 * 2 ** 20
+
+
+def log(*args):
+    print(*args, file=sys.stderr, flush=True)
+
+
+def parse_args():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--workload", default="north", choices=["north", "cfg2", "cfg3", "cfg4", "cfg1"])
+    p.add_argument("--secondary", default="cfg2", help="second workload to report ('' for none)")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
+    return p.parse_args()
+
+
+class Setup:
+    """Rotating cache pools, the batch metadata and per-step new tokens of one workload."""
+
+    def __init__(self, name: str, device):
+        import torch as t
+        from aiproj_amd import workloads
+        from aiproj_amd.inference.paged_kv_cache import PagedKVCache
+        import oracle
+
+        self.spec = workloads.spec(name)
+        s = self.spec
+        self.w = workloads.build(s, device)
+        self.context = workloads.make_context(self.w)
+        self.decode_bytes = oracle.decode_algorithmic_bytes(s.lengths, s.num_q_heads, s.num_kv_heads,
+                                                            s.head_dim, s.block_size)
+        self.append_bytes = oracle.append_algorithmic_bytes(s.batch, s.num_kv_heads, s.head_dim, in_bytes=2)
+        pool_bytes = self.w.num_blocks * s.block_size * s.num_kv_heads * (2 * s.head_dim + 8)
+        self.num_pools = max(2, math.ceil(2 * MALL_BYTES / pool_bytes) + 1)
+        self.pool_bytes = pool_bytes
+        self.caches = []
+        for _ in range(self.num_pools):
+            cache = PagedKVCache(self.w.num_blocks, s.block_size, s.num_kv_heads, s.head_dim, device, t.float8_e4m3fn)
+            workloads.fill_cache(self.w, cache, device)
+            self.caches.append(cache)
+        self.new_tokens = [workloads.new_kv(self.w, device, step) for step in range(4)]
+        t.cuda.synchronize()
+
+    def step(self, i: int):
+        from aiproj_amd.kernals.decode_attention import decode_attention_wrapper
+
+        cache = self.caches[i % self.num_pools]
+        k, v = self.new_tokens[i % len(self.new_tokens)]
+        cache.append_kv(self.w.new_blocks, self.w.new_offsets, k, v)
+        return decode_attention_wrapper(self.w.q, cache, self.context)
+
+
+def time_steps(setup: Setup, steps: int, warmup: int):
+    """(ms per step, mean split-kernel ms) over `steps` timed steps after `warmup`."""
+    import ctypes
+    import torch as t
+    from aiproj_amd import _native
+
+    lib = _native.lib()
+    for i in range(warmup):
+        setup.step(i)
+    t.cuda.synchronize()
+    _native.check(lib.kvfp8_timing_enable(steps), "kvfp8_timing_enable")
+    start, end = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+    t.cuda.synchronize()
+    start.record()
+    for i in range(steps):
+        setup.step(warmup + i)
+    end.record()
+    t.cuda.synchronize()
+    total_ms = ctypes.c_double(0.0)
+    launches = ctypes.c_int64(0)
+    _native.check(lib.kvfp8_timing_read(ctypes.byref(total_ms), ctypes.byref(launches)), "kvfp8_timing_read")
+    kernel_ms = total_ms.value / max(1, launches.value)
+    return start.elapsed_time(end) / steps, kernel_ms, launches.value
+
+
+def copy_bandwidth_gbs(nbytes: int = 2 * 2 ** 30) -> float:
+    """Device-to-device copy of nbytes (read + write), the practical HBM roofline."""
+    import torch as t
+
+    src = t.empty(nbytes, dtype=t.uint8, device="cuda")
+    dst = t.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    t.cuda.synchronize()
+    start, end = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(10):
+        dst.copy_(src)
+    end.record()
+    t.cuda.synchronize()
+    ms = start.elapsed_time(end) / 10
+    del src, dst
+    t.cuda.empty_cache()
+    return 2 * nbytes / (ms * 1e-3) / 1e9
+
+
+def cpu_baseline(setup: Setup, budget_s: float):
+    """The oracle (numpy restatement of the reference's CPU path) on a bounded sample:
+    quantize-and-scatter the new tokens, then gather, dequantize and attend for the
+    first n sequences, on host copies of the same inputs."""
+    import numpy as np
+    import torch as t
+    import oracle
+
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([info.get("num_threads", 1) for info in threadpool_info()] or [1])
+    except Exception:  # noqa: BLE001 - report what can be measured
+        threads = os.cpu_count() or 1
+
+    s = setup.spec
+    cache = setup.caches[0]
+    kc = cache.k.view(t.uint8).cpu().numpy().copy()
+    vc = cache.v.view(t.uint8).cpu().numpy().copy()
+    ks = cache.k_scales.cpu().numpy().copy()
+    vs = cache.v_scales.cpu().numpy().copy()
+    table = setup.w.block_table.cpu().numpy()
+    q = setup.w.q.float().cpu().numpy()
+    new_k, new_v = (x.float().cpu().numpy() for x in setup.new_tokens[0])
+    new_blocks = setup.w.new_blocks.cpu().numpy()
+    new_offsets = setup.w.new_offsets.cpu().numpy()
+
+    # Size the sample from one timed sequence so the leg stays within the budget.
+    t0 = time.perf_counter()
+    oracle.paged_decode(q[:1], kc, vc, ks, vs, table, [0], s.lengths[:1], s.block_size)
+    per_seq = max(time.perf_counter() - t0, 1e-3)
+    n = int(max(1, min(s.batch, budget_s / 3 / per_seq)))
+    reps = 3
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        oracle.scatter_append(kc, vc, ks, vs, new_k[:n], new_v[:n], new_blocks[:n], new_offsets[:n])
+        oracle.paged_decode(q[:n], kc, vc, ks, vs, table, np.arange(n), s.lengths[:n], s.block_size)
+        times.append(time.perf_counter() - t0)
+    sec = float(np.median(times))
+    nbytes = (oracle.decode_algorithmic_bytes(s.lengths[:n], s.num_q_heads, s.num_kv_heads, s.head_dim,
+                                              s.block_size)
+              + oracle.append_algorithmic_bytes(n, s.num_kv_heads, s.head_dim))
+    return {
+        "value": round(nbytes / sec / 1e9, 3),
+        "unit": "GB/s",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": (f"numpy oracle (float64 attention) on {n} of {s.batch} sequences of the {s.name} step "
+                   f"({sum(s.lengths[:n])} KV tokens), median of {reps} reps, {sec:.2f} s each"),
+        "kv_tokens_per_s": round(sum(s.lengths[:n]) / sec, 1),
+        "host_cpu_count": os.cpu_count(),
+        "host_cpu": platform.processor() or platform.machine(),
+    }
+
+
+def traffic_for(kernel: str, workload: str):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if measured."""
+    path = ROOT / "profiles" / f"{kernel}_{workload}_traffic.json"
+    if not path.exists():
+        return None
+    return json.loads(path.read_text()).get("hbm_bytes_per_launch")
+
+
+def measure(name: str, steps: int, warmup: int):
+    import torch as t
+
+    setup = Setup(name, "cuda")
+    ms, kernel_ms, launches = time_steps(setup, steps, warmup)
+    s = setup.spec
+    result = {
+        "setup": setup,
+        "ms_per_step": ms,
+        "split_kernel_ms": kernel_ms,
+        "timed_launches": launches,
+        "step_bytes": setup.decode_bytes + setup.append_bytes,
+        "gbs": (setup.decode_bytes + setup.append_bytes) / (ms * 1e-3) / 1e9,
+        "kernel_gbs": setup.decode_bytes / (kernel_ms * 1e-3) / 1e9,
+        "kv_tokens_per_s": s.total_tokens / (ms * 1e-3),
+        "pools": setup.num_pools,
+        "pool_mb": setup.pool_bytes / 1e6,
+    }
+    log(f"[{name}] B={s.batch} Hq={s.num_q_heads} Hkv={s.num_kv_heads} D={s.head_dim} tokens={s.total_tokens} "
+        f"pools={setup.num_pools}x{setup.pool_bytes / 1e6:.0f}MB: {ms * 1e3:.1f} us/step, "
+        f"split kernel {kernel_ms * 1e3:.1f} us ({result['kernel_gbs']:.0f} GB/s), "
+        f"step {result['gbs']:.0f} GB/s")
+    t.cuda.synchronize()
+    return result
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch as t
+
+    if not t.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    from aiproj_amd import _native
+
+    _native.lib()
+    log(f"device {t.cuda.get_device_name()} torch {t.__version__} lib {_native.lib().kvfp8_version().decode()}")
+
+    copy_gbs = copy_bandwidth_gbs()
+    log(f"device copy bandwidth: {copy_gbs:.0f} GB/s")
+
+    main_result = measure(args.workload, args.steps, args.warmup)
+    secondary = None
+    if args.secondary and args.secondary != args.workload:
+        r = measure(args.secondary, max(10, args.steps // 2), max(3, args.warmup // 2))
+        secondary = {
+            "workload": args.secondary,
+            "lengths": "U[512, 4096] seeded draw" if args.secondary == "cfg2" else "see aiproj_amd/workloads.py",
+            "value": round(r["gbs"], 1),
+            "unit": "GB/s",
+            "pct_of_peak": round(100 * r["gbs"] / PEAK_HBM_GBS, 2),
+            "kv_tokens_per_s": round(r["kv_tokens_per_s"]),
+            "ms_per_step": round(r["ms_per_step"], 5),
+            "split_kernel_us": round(r["split_kernel_ms"] * 1e3, 2),
+            "split_kernel_gbs": round(r["kernel_gbs"], 1),
+        }
+        del r
+
+    s = main_result["setup"].spec
+    cpu = None if args.no_cpu else cpu_baseline(main_result["setup"], args.cpu_seconds)
+    kernel_gbs = main_result["kernel_gbs"]
+    line = {
+        "metric": METRIC,
+        "value": round(main_result["gbs"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(main_result["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8_e4m3fn",
+        "data": "synthetic (seeded N(0,1) bf16 K/V quantized to e4m3fn, bf16 q)",
+        "config": {
+            "workload": (f"{s.name}: B={s.batch}, {s.num_q_heads}q/{s.num_kv_heads}kv heads, D={s.head_dim}, "
+                         f"page {s.block_size}, contexts {min(s.lengths)}..{max(s.lengths)} "
+                         f"(total {s.total_tokens} KV tokens), FP8 e4m3fn paged cache with per-(page slot, "
+                         f"kv head) scales, shuffled page pool; step = 1-token quantized append + decode"),
+            "pools_rotated": main_result["pools"],
+            "pool_mb": round(main_result["pool_mb"], 1),
+        },
+        "pct_of_peak": round(100 * main_result["gbs"] / PEAK_HBM_GBS, 2),
+        "kv_tokens_per_s": round(main_result["kv_tokens_per_s"]),
+        "copy_gbs": round(copy_gbs, 1),
+        "pct_of_copy": round(100 * main_result["gbs"] / copy_gbs, 2),
+        "roofline": {
+            "kernel": "decode split kernel",
+            "bound": "hbm",
+            "achieved": round(kernel_gbs, 1),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(kernel_gbs / PEAK_HBM_GBS, 4),
+            "traffic": traffic_for("decode_split", s.name),
+            "algorithmic_bytes_per_launch": main_result["setup"].decode_bytes,
+            "mean_launch_us": round(main_result["split_kernel_ms"] * 1e3, 2),
+        },
+        "cpu_baseline": cpu,
+        "secondary": secondary,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,233 @@
+"""HIP quantize-and-scatter append vs the oracle (GPU).
+
+Mirrors section E of reference tests/test_kv_cache_quantization.py:242-391, with a
+stricter bar: codes and scales must be bit-identical to the torch/numpy oracle
+(the reference allowed 1% code mismatch for its Triton division).
+"""
+
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch as t
+
+import oracle
+from aiproj_amd.inference.page_allocator import PageAllocator
+from aiproj_amd.inference.paged_kv_cache import PagedKVCache
+from tests.helpers import FP8, error_bound, scattered_locations, torch_reference_quantize
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def stored(cache, blocks, offsets):
+    """(k codes, k scales, v codes, v scales) at the given locations, as numpy."""
+    return (cache.k[blocks, offsets].view(t.uint8).cpu().numpy(), cache.k_scales[blocks, offsets].cpu().numpy(),
+            cache.v[blocks, offsets].view(t.uint8).cpu().numpy(), cache.v_scales[blocks, offsets].cpu().numpy())
+
+
+def assert_bit_exact(cache, blocks, offsets, ks, vs):
+    kc, ksc, vc, vsc = stored(cache, blocks, offsets)
+    for x, codes, scales in ((ks, kc, ksc), (vs, vc, vsc)):
+        ref_codes, ref_scales = torch_reference_quantize(x.cpu())
+        assert np.array_equal(scales.view(np.uint32), ref_scales.view(np.uint32))
+        mismatch = codes != ref_codes
+        assert not mismatch.any(), f"{mismatch.sum()} of {codes.size} codes differ"
+        o_codes, o_scales = oracle.quantize(x.float().cpu().numpy())
+        assert np.array_equal(codes, o_codes) and np.array_equal(scales, o_scales)
+
+
+@t.inference_mode()
+@pytest.mark.parametrize("input_dtype", [t.float32, t.float16, t.bfloat16])
+@pytest.mark.parametrize("head_dim", [16, 64, 80, 128, 256])
+def test_fp8_append_is_bit_exact(input_dtype, head_dim):
+    t.manual_seed(2)
+    num_blocks, block_size, num_kv_heads, num_tokens = 16, 16, 4, 100
+    cache = PagedKVCache(num_blocks, block_size, num_kv_heads, head_dim, "cuda", FP8)
+    blocks, offsets = scattered_locations(num_tokens, num_blocks, block_size, "cuda")
+    ks = (t.randn(num_tokens, num_kv_heads, head_dim, device="cuda") * 3).to(input_dtype)
+    vs = t.randn(num_tokens, num_kv_heads, head_dim, device="cuda").to(input_dtype)
+    cache.append_kv(blocks, offsets, ks, vs)
+    assert_bit_exact(cache, blocks, offsets, ks, vs)
+
+
+@t.inference_mode()
+def test_fp8_append_writes_only_targeted_slots():
+    cache = PagedKVCache(8, 4, 2, 32, "cuda", FP8)
+    cache.k.copy_(t.full(cache.k.shape, 5.0, device="cuda").to(FP8))
+    cache.v.copy_(t.full(cache.v.shape, 5.0, device="cuda").to(FP8))
+    cache.k_scales.fill_(-1.0)
+    cache.v_scales.fill_(-1.0)
+    blocks, offsets = scattered_locations(11, 8, 4, "cuda")
+    cache.append_kv(blocks, offsets, t.randn(11, 2, 32, device="cuda"), t.randn(11, 2, 32, device="cuda"))
+    written = t.zeros(8, 4, dtype=t.bool, device="cuda")
+    written[blocks, offsets] = True
+    for storage in (cache.k, cache.v):
+        assert (storage[~written].float() == 5.0).all()
+    for scales in (cache.k_scales, cache.v_scales):
+        assert (scales[~written] == -1.0).all()
+        assert (scales[written] > 0).all()
+
+
+@t.inference_mode()
+def test_fp8_append_accepts_non_contiguous_input():
+    t.manual_seed(3)
+    cache = PagedKVCache(8, 4, 2, 32, "cuda", FP8)
+    blocks, offsets = scattered_locations(10, 8, 4, "cuda")
+    ks = t.randn(2, 10, 32, device="cuda").transpose(0, 1)
+    vs = t.randn(2, 10, 32, device="cuda").transpose(0, 1)
+    assert not ks.is_contiguous()
+    cache.append_kv(blocks, offsets, ks, vs)
+    assert_bit_exact(cache, blocks, offsets, ks, vs)
+    # A view whose last dimension is strided is copied, not misread.
+    ks2 = t.randn(10, 32, 2, device="cuda").transpose(1, 2)
+    cache.append_kv(blocks, offsets, ks2, ks2)
+    assert_bit_exact(cache, blocks, offsets, ks2, ks2)
+
+
+@t.inference_mode()
+@pytest.mark.parametrize("input_dtype,peak", [(t.float32, 1e30), (t.float32, 1e-30), (t.float16, 65504.0),
+                                              (t.bfloat16, 1e30)])
+def test_fp8_append_extreme_magnitudes(input_dtype, peak):
+    t.manual_seed(4)
+    cache = PagedKVCache(8, 8, 2, 64, "cuda", FP8)
+    blocks, offsets = scattered_locations(40, 8, 8, "cuda")
+    x = t.randn(40, 2, 64, device="cuda", dtype=t.float64)
+    x = (x / x.abs().amax(-1, keepdim=True) * peak).to(input_dtype)
+    cache.append_kv(blocks, offsets, x, x)
+    assert_bit_exact(cache, blocks, offsets, x, x)
+    k = cache.k[blocks, offsets].float() * cache.k_scales[blocks, offsets].unsqueeze(-1)
+    assert t.isfinite(k).all()
+    assert (cache.k_scales[blocks, offsets] > 0).all()
+
+
+@t.inference_mode()
+def test_fp8_append_zero_vectors():
+    cache = PagedKVCache(4, 4, 2, 16, "cuda", FP8)
+    blocks, offsets = scattered_locations(5, 4, 4, "cuda")
+    zeros = t.zeros(5, 2, 16, device="cuda")
+    cache.append_kv(blocks, offsets, zeros, zeros)
+    assert (cache.k_scales[blocks, offsets] == 1.0).all()
+    assert (cache.k[blocks, offsets].float() == 0).all()
+
+
+@t.inference_mode()
+def test_fp8_append_nan_rows_follow_torch():
+    cache = PagedKVCache(4, 4, 1, 16, "cuda", FP8)
+    blocks, offsets = scattered_locations(3, 4, 4, "cuda")
+    x = t.randn(3, 1, 16, device="cuda")
+    x[1, 0, 5] = float("nan")
+    x[2, 0, 0] = -float("nan")
+    cache.append_kv(blocks, offsets, x, x)
+    assert_bit_exact(cache, blocks, offsets, x, x)
+
+
+@t.inference_mode()
+def test_fp8_append_through_cache_manager_round_trips():
+    t.manual_seed(5)
+    manager = PageAllocator(16, 4, 2, 32, "cuda")
+    cache = PagedKVCache(16, 4, 2, 32, "cuda", FP8)
+    length = 13
+    slot = manager.allocate_request(0, length)
+    ks = t.randn(length, 2, 32, device="cuda", dtype=t.bfloat16)
+    vs = t.randn_like(ks)
+    manager.append_request(0, t.arange(length, device="cuda"), ks, vs, cache)
+    positions = t.arange(length, device="cuda")
+    blocks = manager.block_table[slot, positions // 4]
+    offsets = positions % 4
+    assert_bit_exact(cache, blocks, offsets, ks, vs)
+    k = (cache.k[blocks, offsets].float() * cache.k_scales[blocks, offsets].unsqueeze(-1)).cpu().numpy()
+    _, k_scales = oracle.quantize(ks.float().cpu().numpy())
+    assert (np.abs(ks.float().cpu().numpy() - k) <= 2 * error_bound(ks.float().cpu().numpy(), k_scales)).all()
+
+
+@t.inference_mode()
+@pytest.mark.parametrize("index_dtype", [t.int32, t.int64])
+def test_fp8_append_index_dtypes_and_out_of_pool_rows(index_dtype):
+    cache = PagedKVCache(6, 4, 2, 64, "cuda", FP8)
+    cache.k.view(t.uint8).fill_(0x11)
+    cache.k_scales.fill_(-2.0)
+    blocks = t.tensor([0, 5, -1, 6, 2, 1], dtype=index_dtype, device="cuda")
+    offsets = t.tensor([3, 0, 1, 1, 4, 2], dtype=index_dtype, device="cuda")   # rows 2, 3, 4 are outside
+    x = t.randn(6, 2, 64, device="cuda")
+    cache.append_kv(blocks, offsets, x, x)
+    good = t.tensor([0, 1, 5], device="cuda")
+    assert_bit_exact(cache, blocks[good].long(), offsets[good].long(), x[good], x[good])
+    written = t.zeros(6, 4, dtype=t.bool)
+    written[[0, 5, 1], [3, 0, 2]] = True
+    assert (cache.k.view(t.uint8)[~written.cuda()] == 0x11).all()
+    assert (cache.k_scales[~written.cuda()] == -2.0).all()
+
+
+@t.inference_mode()
+def test_golden_quantize_cases_on_gpu():
+    cases = np.load(GOLDEN / "quantize_cases.npz")
+    for name in sorted({key.split("__")[0] for key in cases.files}):
+        x = cases[f"{name}__x"]
+        dtype = {"torch.float32": t.float32, "torch.float16": t.float16,
+                 "torch.bfloat16": t.bfloat16}[str(cases[f"{name}__dtype"])]
+        rows = x.reshape(-1, x.shape[-1])
+        n, d = rows.shape
+        cache = PagedKVCache(-(-n // 16), 16, 1, d, "cuda", FP8)
+        flat = t.arange(n, device="cuda")
+        xt = t.from_numpy(rows).to(dtype).cuda().unsqueeze(1)
+        cache.append_kv(flat // 16, flat % 16, xt, xt)
+        codes = cache.k.view(t.uint8).reshape(-1, d)[:n].cpu().numpy()
+        scales = cache.k_scales.reshape(-1)[:n].cpu().numpy()
+        assert np.array_equal(codes, cases[f"{name}__codes"].reshape(-1, d)), name
+        assert np.array_equal(scales.view(np.uint32), cases[f"{name}__scales"].reshape(-1).view(np.uint32)), name
+
+
+@t.inference_mode()
+@pytest.mark.parametrize("input_dtype", [t.bfloat16, t.float32])
+def test_fp8_append_large_random_sweep_is_bit_exact(input_dtype):
+    # 262144 rows over 16 decades of magnitude: every division and rounding path.
+    g = t.Generator(device="cuda").manual_seed(11)
+    rows, d = 1 << 18, 128
+    scale = t.logspace(-30, 30, rows, device="cuda").view(-1, 1, 1)
+    x = (t.randn(rows, 1, d, device="cuda", generator=g) * scale).to(input_dtype)
+    cache = PagedKVCache(rows // 16, 16, 1, d, "cuda", FP8)
+    flat = t.arange(rows, device="cuda")
+    cache.append_kv(flat // 16, flat % 16, x, x)
+    codes = cache.k.view(t.uint8).reshape(rows, d).cpu().numpy()
+    scales = cache.k_scales.reshape(rows).cpu().numpy()
+    o_codes, o_scales = oracle.quantize(x.float().cpu().numpy().reshape(rows, d))
+    assert np.array_equal(scales.view(np.uint32), o_scales.view(np.uint32))
+    assert np.array_equal(codes, o_codes), f"{(codes != o_codes).sum()} codes differ"
+
+
+@t.inference_mode()
+@pytest.mark.parametrize("cache_dtype", [t.float16, t.bfloat16, t.float32])
+@pytest.mark.parametrize("input_dtype", [t.float32, t.bfloat16])
+def test_unquantized_device_append(cache_dtype, input_dtype):
+    cache = PagedKVCache(6, 4, 2, 80, "cuda", cache_dtype)
+    cache.k.fill_(-7.0)
+    cache.v.fill_(-7.0)
+    blocks, offsets = scattered_locations(9, 6, 4, "cuda")
+    ks = t.randn(9, 2, 80, device="cuda").to(input_dtype)
+    vs = t.randn(9, 2, 80, device="cuda").to(input_dtype)
+    cache.append_kv(blocks, offsets, ks, vs)
+    assert t.equal(cache.k[blocks, offsets], ks.to(cache_dtype))
+    assert t.equal(cache.v[blocks, offsets], vs.to(cache_dtype))
+    written = t.zeros(6, 4, dtype=t.bool, device="cuda")
+    written[blocks, offsets] = True
+    assert (cache.k[~written] == -7.0).all()
+
+
+@t.inference_mode()
+def test_golden_cfg1_cache_bytes():
+    g = np.load(GOLDEN / "cfg1_decode.npz")
+    nb = int(g["num_blocks"])
+    hkv, d = g["k_codes"].shape[1:]
+    cache = PagedKVCache(nb, 16, int(hkv), int(d), "cuda", FP8)
+    ks = t.from_numpy(g["ks_bf16_bits"]).view(t.bfloat16).cuda()
+    vs = t.from_numpy(g["vs_bf16_bits"]).view(t.bfloat16).cuda()
+    blocks = t.from_numpy(g["blocks"]).cuda()
+    offsets = t.from_numpy(g["offsets"]).cuda()
+    cache.append_kv(blocks, offsets, ks, vs)
+    kc, ksc, vc, vsc = stored(cache, blocks, offsets)
+    assert np.array_equal(kc, g["k_codes"]) and np.array_equal(vc, g["v_codes"])
+    assert np.array_equal(ksc.view(np.uint32), g["k_scales"].view(np.uint32))
+    assert np.array_equal(vsc.view(np.uint32), g["v_scales"].view(np.uint32))

@@ -1,0 +1,120 @@
+"""The C-ABI library on the CPU: it loads, exports every symbol include/kvfp8.h declares,
+its host-run copy of the device encoding code equals the oracle, and host-side
+argument checks return the documented codes without touching a GPU."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle
+from aiproj_amd import _native
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "kvfp8.h"
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _native.lib()
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(kvfp8_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol(lib):
+    names = declared_functions()
+    assert len(names) >= 8
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(_native.SIGNATURES)
+    assert lib.kvfp8_version().decode().endswith("gfx950")
+
+
+def test_strerror_names_every_code(lib):
+    for code in range(0, -7, -1):
+        assert _native.strerror(code) not in ("", "unknown error")
+
+
+def _host_encode(lib, x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint8)
+    lib.kvfp8_host_encode_e4m3fn(x.ctypes.data, out.ctypes.data, x.size)
+    return out
+
+
+def test_device_encoder_equals_oracle_on_strided_fp32_sweep(lib):
+    for start in range(0, 2 ** 32, 2 ** 28):
+        bits = np.arange(start, start + 2 ** 28, 251, dtype=np.uint64).astype(np.uint32)
+        x = bits.view(np.float32)
+        assert np.array_equal(_host_encode(lib, x), oracle.f32_to_e4m3fn(x)), hex(start)
+
+
+def test_device_encoder_equals_oracle_on_every_bf16_value(lib):
+    x = (np.arange(2 ** 16, dtype=np.uint32) << 16).view(np.float32)
+    assert np.array_equal(_host_encode(lib, x), oracle.f32_to_e4m3fn(x))
+
+
+def test_device_quantizer_equals_golden(lib):
+    cases = np.load(Path(__file__).resolve().parent / "golden" / "quantize_cases.npz")
+    for name in sorted({key.split("__")[0] for key in cases.files}):
+        x = np.ascontiguousarray(cases[f"{name}__x"], dtype=np.float32)
+        d = x.shape[-1]
+        rows = x.size // d
+        codes = np.empty(x.shape, dtype=np.uint8)
+        scales = np.empty(x.shape[:-1], dtype=np.float32)
+        lib.kvfp8_host_quantize_rows(x.ctypes.data, rows, d, codes.ctypes.data, scales.ctypes.data)
+        assert np.array_equal(codes, cases[f"{name}__codes"]), name
+        assert np.array_equal(scales.view(np.uint32), cases[f"{name}__scales"].view(np.uint32)), name
+
+
+def test_workspace_size_depends_on_shapes_only(lib):
+    a = lib.kvfp8_decode_workspace_bytes(32, 32, 8, 128, 257, 16, _native.E4M3FN)
+    b = lib.kvfp8_decode_workspace_bytes(32, 32, 8, 128, 257, 16, _native.E4M3FN)
+    assert a == b > 0
+    assert lib.kvfp8_decode_workspace_bytes(0, 32, 8, 128, 257, 16, _native.E4M3FN) == 0
+
+
+def test_argument_errors_are_reported_before_any_launch(lib):
+    fake = ctypes.c_void_p(16)    # never dereferenced: every call below fails host checks
+    # Bad q dtype.
+    rc = lib.kvfp8_paged_decode(fake, 9, 0, 0, 1, 8, 2, 64, fake, fake, _native.E4M3FN, fake, fake,
+                                4, 16, fake, 1, 1, fake, _native.I64, fake, _native.I32, 0.125,
+                                fake, fake, 1 << 20, None)
+    assert rc == -1
+    # Hq not a multiple of Hkv.
+    rc = lib.kvfp8_paged_decode(fake, _native.BF16, 0, 0, 1, 6, 4, 64, fake, fake, _native.E4M3FN, fake, fake,
+                                4, 16, fake, 1, 1, fake, _native.I64, fake, _native.I32, 0.125,
+                                fake, fake, 1 << 20, None)
+    assert rc == -2
+    # Block size not a power of two.
+    rc = lib.kvfp8_paged_decode(fake, _native.BF16, 0, 0, 1, 8, 2, 64, fake, fake, _native.E4M3FN, fake, fake,
+                                4, 12, fake, 1, 1, fake, _native.I64, fake, _native.I32, 0.125,
+                                fake, fake, 1 << 20, None)
+    assert rc == -2
+    # FP8 cache without scales.
+    rc = lib.kvfp8_paged_decode(fake, _native.BF16, 0, 0, 1, 8, 2, 64, fake, fake, _native.E4M3FN, None, None,
+                                4, 16, fake, 1, 1, fake, _native.I64, fake, _native.I32, 0.125,
+                                fake, fake, 1 << 20, None)
+    assert rc == -4
+    # Workspace too small.
+    rc = lib.kvfp8_paged_decode(fake, _native.BF16, 0, 0, 4, 8, 2, 64, fake, fake, _native.E4M3FN, fake, fake,
+                                4, 16, fake, 4, 64, fake, _native.I64, fake, _native.I32, 0.125,
+                                fake, fake, 16, None)
+    assert rc == -5
+    # Append: bad index dtype, bad input dtype.
+    rc = lib.kvfp8_quantize_append(fake, fake, _native.BF16, 0, 0, 0, 0, fake, _native.F32, fake, _native.I32,
+                                   1, 2, 64, 4, 16, fake, fake, fake, fake, None)
+    assert rc == -1
+    rc = lib.kvfp8_quantize_append(fake, fake, _native.E4M3FN, 0, 0, 0, 0, fake, _native.I32, fake, _native.I32,
+                                   1, 2, 64, 4, 16, fake, fake, fake, fake, None)
+    assert rc == -1
+    # Empty batches are a no-op.
+    assert lib.kvfp8_quantize_append(fake, fake, _native.BF16, 0, 0, 0, 0, fake, _native.I32, fake, _native.I32,
+                                     0, 2, 64, 4, 16, fake, fake, fake, fake, None) == 0
