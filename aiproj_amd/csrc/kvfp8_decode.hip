@@ -204,18 +204,16 @@ namespace {
 
 struct Plan {
     bool mfma;
-    int32_t chunk_tokens;
+    int32_t chunk_tokens;   // generic kernel
     int32_t max_chunks;
-    int32_t units;      // head units per chunk: q heads (generic) or kv heads (MFMA)
 };
 
 Plan make_plan(int32_t batch, int32_t hq, int32_t hkv, int32_t d, int64_t bt_width, int32_t bs, int kv_dtype) {
     Plan p;
-    p.mfma = mfma_decode_supported(hq, hkv, d, kv_dtype);
-    p.chunk_tokens = p.mfma ? mfma_chunk_tokens(batch, hkv, bt_width, bs) : kGenericChunkTokens;
+    p.mfma = mfma_decode_supported(batch, hq, hkv, d, bt_width, bs, kv_dtype);
+    p.chunk_tokens = kGenericChunkTokens;
     const int64_t cap = bt_width * bs;
     p.max_chunks = (int32_t)((cap + p.chunk_tokens - 1) / p.chunk_tokens);
-    p.units = p.mfma ? hkv : hq;
     return p;
 }
 
@@ -229,9 +227,21 @@ int ilog2(int64_t x) {
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-int64_t workspace_for(const Plan& p, int32_t batch, int32_t hq, int32_t d) {
+int64_t generic_workspace(const Plan& p, int32_t batch, int32_t hq, int32_t d) {
     const int64_t states = (int64_t)batch * p.max_chunks * hq;
     return (int64_t)(2 * align256(states * sizeof(float)) + align256(states * d * sizeof(float)));
+}
+
+// The MFMA path falls back to the generic kernel when a pointer is not 16-byte
+// aligned, so its workspace covers both.
+int64_t workspace_for(const Plan& p, int32_t batch, int32_t hq, int32_t hkv, int32_t d) {
+    int64_t need = generic_workspace(p, batch, hq, d);
+    if (p.mfma) {
+        int64_t off[4];
+        const int64_t m = mfma_workspace_layout(batch, hq, hkv, d, off);
+        need = need > m ? need : m;
+    }
+    return need;
 }
 
 template <int KVT, int QT>
@@ -274,19 +284,17 @@ void timing_after(hipStream_t s) {
 }
 
 template <int QT>
-hipError_t dispatch_kv(const DecodeArgs& a, int kv_dtype, const Plan& p, hipStream_t s) {
-    const int64_t units_total = (int64_t)a.batch * p.max_chunks * p.units;
+hipError_t dispatch_kv(const DecodeArgs& a, int kv_dtype, const Plan& p, void* workspace, hipStream_t s) {
+    const bool aligned = (((uintptr_t)a.k_cache | (uintptr_t)a.v_cache) & 15) == 0;
+    if (p.mfma && aligned) return launch_mfma_decode<QT>(a, workspace, s, timing_before, timing_after);
+    const int64_t units_total = (int64_t)a.batch * p.max_chunks * a.num_q_heads;
     hipError_t err;
     timing_before(s);
-    if (p.mfma) {
-        err = launch_mfma_decode<QT>(a, units_total, s);
-    } else {
-        switch (kv_dtype) {
-            case KVFP8_E4M3FN: err = launch_generic<KVFP8_E4M3FN, QT>(a, units_total, s); break;
-            case KVFP8_BF16: err = launch_generic<KVFP8_BF16, QT>(a, units_total, s); break;
-            case KVFP8_F16: err = launch_generic<KVFP8_F16, QT>(a, units_total, s); break;
-            default: err = launch_generic<KVFP8_F32, QT>(a, units_total, s); break;
-        }
+    switch (kv_dtype) {
+        case KVFP8_E4M3FN: err = launch_generic<KVFP8_E4M3FN, QT>(a, units_total, s); break;
+        case KVFP8_BF16: err = launch_generic<KVFP8_BF16, QT>(a, units_total, s); break;
+        case KVFP8_F16: err = launch_generic<KVFP8_F16, QT>(a, units_total, s); break;
+        default: err = launch_generic<KVFP8_F32, QT>(a, units_total, s); break;
     }
     timing_after(s);
     if (err != hipSuccess) return err;
@@ -302,7 +310,7 @@ extern "C" int64_t kvfp8_decode_workspace_bytes(int32_t batch, int32_t num_q_hea
         block_size <= 0)
         return 0;
     const Plan p = make_plan(batch, num_q_heads, num_kv_heads, head_dim, bt_width, block_size, kv_dtype);
-    return workspace_for(p, batch, num_q_heads, head_dim);
+    return workspace_for(p, batch, num_q_heads, num_kv_heads, head_dim);
 }
 
 extern "C" int kvfp8_paged_decode(const void* q, int q_dtype, int64_t q_stride_b, int64_t q_stride_h,
@@ -327,7 +335,7 @@ extern "C" int kvfp8_paged_decode(const void* q, int q_dtype, int64_t q_stride_b
     if (kv_dtype == KVFP8_E4M3FN && (!k_scales || !v_scales)) return KVFP8_ENULL;
 
     const Plan p = make_plan(batch, num_q_heads, num_kv_heads, head_dim, bt_width, block_size, kv_dtype);
-    const int64_t need = workspace_for(p, batch, num_q_heads, head_dim);
+    const int64_t need = workspace_for(p, batch, num_q_heads, num_kv_heads, head_dim);
     if (!workspace || workspace_bytes < need) return KVFP8_EWORKSPACE;
 
     const int64_t states = (int64_t)batch * p.max_chunks * num_q_heads;
@@ -365,9 +373,9 @@ extern "C" int kvfp8_paged_decode(const void* q, int q_dtype, int64_t q_stride_b
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     hipError_t err;
     switch (q_dtype) {
-        case KVFP8_F32: err = dispatch_kv<KVFP8_F32>(a, kv_dtype, p, s); break;
-        case KVFP8_F16: err = dispatch_kv<KVFP8_F16>(a, kv_dtype, p, s); break;
-        default: err = dispatch_kv<KVFP8_BF16>(a, kv_dtype, p, s); break;
+        case KVFP8_F32: err = dispatch_kv<KVFP8_F32>(a, kv_dtype, p, workspace, s); break;
+        case KVFP8_F16: err = dispatch_kv<KVFP8_F16>(a, kv_dtype, p, workspace, s); break;
+        default: err = dispatch_kv<KVFP8_BF16>(a, kv_dtype, p, workspace, s); break;
     }
     return (int)err;
 }

@@ -5,13 +5,18 @@
 
 namespace kvfp8 {
 
-// Shapes the MFMA kernel handles; everything else goes to the generic kernel.
-bool mfma_decode_supported(int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int kv_dtype);
+// Shapes the MFMA kernel handles (e4m3fn cache, D in {64, 128}, page size a
+// multiple of 16, group size <= 16); everything else goes to the generic kernel.
+bool mfma_decode_supported(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                           int64_t bt_width, int32_t block_size, int kv_dtype);
 
-// Tokens per work item, chosen from shapes only.
-int32_t mfma_chunk_tokens(int32_t batch, int32_t num_kv_heads, int64_t bt_width, int32_t block_size);
+// Workspace bytes of the MFMA path (tile prefix, then two partial softmax states
+// per workgroup); offsets[0..3] receive the byte offsets of plan, m, l and acc.
+int64_t mfma_workspace_layout(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                              int64_t offsets[4]);
 
 template <int QT>
-hipError_t launch_mfma_decode(const DecodeArgs& a, int64_t units_total, hipStream_t stream);
+hipError_t launch_mfma_decode(const DecodeArgs& a, void* workspace, hipStream_t stream,
+                              void (*before)(hipStream_t), void (*after)(hipStream_t));
 
 }  // namespace kvfp8

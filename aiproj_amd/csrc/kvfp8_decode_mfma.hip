@@ -1,17 +1,603 @@
-// FP8 paged decode on the gfx950 matrix cores.
+// FP8 paged decode attention on the gfx950 matrix cores.
+//
+// Replaces the Triton split and reduction kernels of reference
+// src/torch_llm/kernals/decode_attention.py:194-550 for e4m3fn caches with
+// D in {64, 128} and pages of 16k tokens.
+//
+// Work split. The attended tokens of the batch form one list of 16-token tiles
+// (sequence by sequence, tile prefix built in LDS from context_lengths, no host
+// synchronization). Workgroup w of `groups` takes the contiguous tile range
+// [w W / groups, (w+1) W / groups), so every workgroup reads the same number of
+// bytes whatever the length distribution. A sequence that lies inside one range
+// is finished in place; a sequence cut by range boundaries leaves one partial
+// softmax state per piece (at most two per workgroup: its first and last
+// segment) and the combine kernel merges them.
+//
+// Inside a workgroup wave i serves KV head i (and i + waves, ...), so the
+// workgroup reads whole pages: 16 tokens x Hkv x D contiguous bytes of K and V.
+// One step of a wave covers two tiles (32 tokens) of its head:
+//
+//   scores   S^T[t, g] = K[t, :] . Q[g, :]      MFMA 16x16x32 bf16, A = K codes
+//            converted fp8 -> bf16 (exact), B = Q^T (bf16; f32/f16 q as hi + lo)
+//            then x k_scale[t] x sm_scale x log2(e)   (fp32)
+//   softmax  online, base 2, state per lane = per q head column g
+//   output   O^T[d, g] += V^T[d, t] . P'^T[t, g]    MFMA 16x16x32 bf16,
+//            P' = p x v_scale[t]; V^T from an in-register byte transpose
+//
+// MFMA 16x16x32 bf16 operand layout (lane l, element i, output element j):
+//   A[row = l % 16][k = 8 (l / 16) + i], B[k = 8 (l / 16) + i][col = l % 16],
+//   D[row = 4 (l / 16) + j][col = l % 16].
+// The reduction index of each product may be permuted freely as long as both
+// operands use the same permutation; the kernel picks the permutations that let
+// every lane load long contiguous runs:
+//   * QK: lane l reads 16-byte runs of token (l % 16) at byte 64 c + 16 (l / 16);
+//     bytes 8h..8h+7 of run c feed MFMA 2c + h.
+//   * PV: lane l reads 4C contiguous bytes at column 4C (l % 16) of eight token
+//     rows: tokens 4 (l/16) + i of tile A (i < 4) and of tile B (i >= 4), the
+//     same tokens its QK output column holds. v_perm_b32 pairs rows (2p, 2p+1)
+//     of one column and v_cvt_scalef32_pk_bf16_fp8 widens the pair.
 #include "kvfp8_decode_mfma.h"
 
 namespace kvfp8 {
 
-bool mfma_decode_supported(int32_t, int32_t, int32_t, int) { return false; }
+namespace {
 
-int32_t mfma_chunk_tokens(int32_t, int32_t, int64_t, int32_t) { return 256; }
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kMaxWaves = 8;            // KV heads served by one workgroup at a time
+constexpr int kMaxThreads = 64 * kMaxWaves;
+constexpr int kMinTilesPerGroup = 8;    // a workgroup gets at least 128 tokens per head
+constexpr int kWavesPerCu = 16;         // target waves resident per CU (caps the grid)
+constexpr int kMfmaMaxBatch = 8191;     // LDS tile prefix of (batch + 1) int32
+
+struct MfmaArgs {
+    DecodeArgs d;
+    int32_t tps_shift;   // log2(block_size / 16): 16-token tiles per page
+    int32_t* plan;       // [batch + 1] tile prefix, then the workgroup count used
+    float* part_m;       // [2 * max_groups, Hq]
+    float* part_l;       // [2 * max_groups, Hq]
+    float* part_acc;     // [2 * max_groups, Hq, D]
+};
+
+__device__ __forceinline__ int32_t uniform(int32_t x) { return __builtin_amdgcn_readfirstlane(x); }
+
+__device__ __forceinline__ int64_t uniform64(int64_t x) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int32_t)(uint32_t)x);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int32_t)(uint32_t)((uint64_t)x >> 32));
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+__device__ __forceinline__ bf16x8_t cat8(bf16x2_t a, bf16x2_t b, bf16x2_t c, bf16x2_t d) {
+    const bf16x4_t ab = __builtin_shufflevector(a, b, 0, 1, 2, 3);
+    const bf16x4_t cd = __builtin_shufflevector(c, d, 0, 1, 2, 3);
+    return __builtin_shufflevector(ab, cd, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// Two e4m3fn codes (bytes 0-1 or 2-3 of x) -> two bf16, exact.
+__device__ __forceinline__ bf16x2_t fp8x2_lo(uint32_t x) {
+    return __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(x, 1.0f, false);
+}
+__device__ __forceinline__ bf16x2_t fp8x2_hi(uint32_t x) {
+    return __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(x, 1.0f, true);
+}
+
+// Eight codes (x0 bytes 0..3, then x1) -> bf16x8 in byte order.
+__device__ __forceinline__ bf16x8_t fp8x8(uint32_t x0, uint32_t x1) {
+    return cat8(fp8x2_lo(x0), fp8x2_hi(x0), fp8x2_lo(x1), fp8x2_hi(x1));
+}
+
+__device__ __forceinline__ f32x4_t mma(bf16x8_t a, bf16x8_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Tile prefix over the batch in LDS: prefix[b] = sum_{i<b} ceil(len_i / 16).
+__device__ void build_tile_prefix(const DecodeArgs& a, int32_t* prefix, int32_t* scan) {
+    const int threads = blockDim.x, tid = threadIdx.x;
+    const int per = (a.batch + threads - 1) / threads;
+    const int begin = tid * per;
+    int32_t local = 0;
+    for (int i = 0; i < per; ++i) {
+        const int b = begin + i;
+        if (b < a.batch) {
+            int64_t slot;
+            prefix[b] = local;
+            local += (int32_t)((seq_tokens(a, b, &slot) + 15) >> 4);
+        }
+    }
+    scan[tid] = local;
+    __syncthreads();
+    for (int off = 1; off < threads; off <<= 1) {
+        const int32_t add = tid >= off ? scan[tid - off] : 0;
+        __syncthreads();
+        scan[tid] += add;
+        __syncthreads();
+    }
+    const int32_t base = tid > 0 ? scan[tid - 1] : 0;
+    for (int i = 0; i < per; ++i) {
+        const int b = begin + i;
+        if (b < a.batch) prefix[b] += base;
+    }
+    if (tid == threads - 1) prefix[a.batch] = scan[threads - 1];
+    __syncthreads();
+}
+
+// Global row (page * block_size + token base) of a 16-token tile; 0 when the
+// page entry is outside the pool (the tile's tokens are then masked).
+struct TileRef {
+    int64_t row0;
+    int32_t valid;
+};
+
+__device__ __forceinline__ TileRef tile_ref(const MfmaArgs& a, const int32_t* table_row, int32_t tile) {
+    const int32_t page = tile >> a.tps_shift;
+    const int64_t phys = table_row[page];
+    const bool ok = phys >= 0 && phys < a.d.num_blocks;
+    const int32_t base = (tile & ((1 << a.tps_shift) - 1)) << 4;
+    TileRef r;
+    r.row0 = ok ? phys * a.d.block_size + base : 0;
+    r.valid = ok;
+    return r;
+}
+
+// Loads of one 32-token step of one KV head.
+template <int C>
+struct StepData {
+    uint4 ka[C];          // tile A: token (l % 16), bytes 64 c + 16 (l / 16) .. + 16
+    uint4 kb[C];          // tile B, same bytes
+    uint32_t v[8][C];     // rows i: token 4 (l/16) + (i % 4) of tile (i < 4 ? A : B), bytes 4C (l % 16) ..
+    float sc;             // lane l: [k|v][tile A|B][token l % 16] scale
+};
+
+template <int C>
+__device__ __forceinline__ void load_step(StepData<C>& s, const MfmaArgs& a, int h, const TileRef& ta,
+                                          const TileRef& tb, int lane) {
+    constexpr int D = 64 * C;
+    constexpr int NB = 4 * C;
+    const int m16 = lane & 15, j = lane >> 4;
+    const int32_t hkv = a.d.num_kv_heads;
+    const int32_t row_stride = hkv * D;
+    const int64_t ea = (ta.row0 * hkv + h) * D;
+    const int64_t eb = (tb.row0 * hkv + h) * D;
+    const uint8_t* kc = reinterpret_cast<const uint8_t*>(a.d.k_cache);
+    const uint8_t* vc = reinterpret_cast<const uint8_t*>(a.d.v_cache);
+    const uint32_t koff = (uint32_t)(m16 * row_stride + 16 * j);
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        s.ka[c] = *reinterpret_cast<const uint4*>(kc + ea + koff + 64 * c);
+        s.kb[c] = *reinterpret_cast<const uint4*>(kc + eb + koff + 64 * c);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint8_t* p = vc + (i < 4 ? ea : eb) + (uint32_t)((4 * j + (i & 3)) * row_stride + NB * m16);
+        if constexpr (C == 1) {
+            s.v[i][0] = *reinterpret_cast<const uint32_t*>(p);
+        } else {
+            const uint2 x = *reinterpret_cast<const uint2*>(p);
+            s.v[i][0] = x.x;
+            s.v[i][1] = x.y;
+        }
+    }
+    const int kv = lane >> 5, which = (lane >> 4) & 1;
+    const int64_t r = (which ? tb.row0 : ta.row0) + m16;
+    s.sc = (kv ? a.d.v_scales : a.d.k_scales)[r * hkv + h];
+}
+
+// Online-softmax state of one wave (one KV head, its G q heads in columns g).
+template <int C>
+struct WaveState {
+    f32x4_t o[4 * C];     // O^T[d = 4C (4 (l/16) + j) + nb][g = l % 16] in o[nb][j]
+    float m;              // running max (base-2 scores) of column g
+    float l;              // this lane's share of the softmax denominator
+};
+
+template <int C, bool kHiLo>
+__device__ __forceinline__ void compute_step(WaveState<C>& st, const StepData<C>& s, const bf16x8_t* qh,
+                                             const bf16x8_t* ql, float4* stage, int lane, int lim_a,
+                                             int lim_b, float score_scale) {
+    const int j = lane >> 4;
+    const bool full = lim_a == 16 && lim_b == 16;   // wave-uniform
+
+    // Scales through this wave's LDS slot: [k|v][tile][token] -> 4 consecutive
+    // tokens per read. The k scale carries sm_scale * log2(e).
+    float* stage_f = reinterpret_cast<float*>(stage);
+    stage_f[lane] = lane < 32 ? s.sc * score_scale : s.sc;
+    __builtin_amdgcn_wave_barrier();
+    const float4 ks_a = stage[j], ks_b = stage[4 + j], vs_a = stage[8 + j], vs_b = stage[12 + j];
+    __builtin_amdgcn_wave_barrier();
+
+    // Scores of the two tiles.
+    f32x4_t sa = {0.0f, 0.0f, 0.0f, 0.0f}, sb = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            const uint32_t* wa = reinterpret_cast<const uint32_t*>(&s.ka[c]);
+            const uint32_t* wb = reinterpret_cast<const uint32_t*>(&s.kb[c]);
+            const bf16x8_t ka = fp8x8(wa[2 * half], wa[2 * half + 1]);
+            const bf16x8_t kb = fp8x8(wb[2 * half], wb[2 * half + 1]);
+            sa = mma(ka, qh[2 * c + half], sa);
+            sb = mma(kb, qh[2 * c + half], sb);
+            if constexpr (kHiLo) {
+                sa = mma(ka, ql[2 * c + half], sa);
+                sb = mma(kb, ql[2 * c + half], sb);
+            }
+        }
+    }
+    float sc[8] = {sa[0] * ks_a.x, sa[1] * ks_a.y, sa[2] * ks_a.z, sa[3] * ks_a.w,
+                   sb[0] * ks_b.x, sb[1] * ks_b.y, sb[2] * ks_b.z, sb[3] * ks_b.w};
+    if (!full) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (4 * j + i >= lim_a) sc[i] = kNegInf;
+            if (4 * j + i >= lim_b) sc[4 + i] = kNegInf;
+        }
+    }
+
+    // Online softmax over the 32 tokens (8 per lane, 4 lane groups per column).
+    float mx = sc[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) mx = fmaxf(mx, sc[i]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(st.m, mx);
+    const float m_use = m_new == kNegInf ? 0.0f : m_new;
+    const float alpha = fast_exp2(st.m - m_use);
+    st.l *= alpha;
+    if (__ballot(alpha != 1.0f)) {
+#pragma unroll
+        for (int nb = 0; nb < 4 * C; ++nb) st.o[nb] *= alpha;
+    }
+    st.m = m_new;
+    const float vs[8] = {vs_a.x, vs_a.y, vs_a.z, vs_a.w, vs_b.x, vs_b.y, vs_b.z, vs_b.w};
+    float pv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float p = fast_exp2(sc[i] - m_use);
+        st.l += p;
+        pv[i] = p * vs[i];
+    }
+    if (!full) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (4 * j + i >= lim_a) pv[i] = 0.0f;
+            if (4 * j + i >= lim_b) pv[4 + i] = 0.0f;
+        }
+    }
+    bf16x8_t ph, pl;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        ph[i] = (__bf16)pv[i];
+        if constexpr (kHiLo) pl[i] = (__bf16)(pv[i] - (float)ph[i]);
+    }
+
+    // V rows: zero the rows of masked tokens (stale pages may hold NaN codes).
+    uint32_t vr[8][C];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const bool live = full || (4 * j + (i & 3) < (i < 4 ? lim_a : lim_b));
+#pragma unroll
+        for (int c = 0; c < C; ++c) vr[i][c] = live ? s.v[i][c] : 0u;
+    }
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        bf16x2_t e[4][4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const uint32_t x = __builtin_amdgcn_perm(vr[2 * p + 1][c], vr[2 * p][c], 0x05010400u);
+            const uint32_t y = __builtin_amdgcn_perm(vr[2 * p + 1][c], vr[2 * p][c], 0x07030602u);
+            e[0][p] = fp8x2_lo(x);
+            e[1][p] = fp8x2_hi(x);
+            e[2][p] = fp8x2_lo(y);
+            e[3][p] = fp8x2_hi(y);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const bf16x8_t av = cat8(e[q][0], e[q][1], e[q][2], e[q][3]);
+            st.o[4 * c + q] = mma(av, ph, st.o[4 * c + q]);
+            if constexpr (kHiLo) st.o[4 * c + q] = mma(av, pl, st.o[4 * c + q]);
+        }
+    }
+}
+
+template <int C, int QT>
+__global__ void __launch_bounds__(kMaxThreads)
+decode_mfma_kernel(MfmaArgs a) {
+    constexpr int D = 64 * C;
+    constexpr int NB = 4 * C;
+    constexpr bool kHiLo = QT != KVFP8_BF16;
+    extern __shared__ int32_t prefix[];                // [batch + 1]
+    __shared__ int32_t scan[kMaxThreads];
+    __shared__ float4 stage_all[kMaxWaves][16];
+
+    build_tile_prefix(a.d, prefix, scan);
+    const int32_t total = prefix[a.d.batch];
+    const int32_t want = (total + kMinTilesPerGroup - 1) / kMinTilesPerGroup;
+    const int32_t groups = min((int32_t)gridDim.x, max(want, 1));
+    if (blockIdx.x == 0) {
+        for (int i = threadIdx.x; i <= a.d.batch; i += blockDim.x) a.plan[i] = prefix[i];
+        if (threadIdx.x == 0) a.plan[a.d.batch + 1] = groups;
+    }
+    const int w = blockIdx.x;
+    if (w >= groups) return;
+    const int32_t start = (int32_t)((int64_t)w * total / groups);
+    const int32_t end = (int32_t)((int64_t)(w + 1) * total / groups);
+
+    const int waves = blockDim.x >> 6;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int m16 = lane & 15, j = lane >> 4;
+    const int G = a.d.num_q_heads / a.d.num_kv_heads;
+    float4* stage = stage_all[wave];
+
+    for (int h = wave; h < a.d.num_kv_heads; h += waves) {
+        int32_t tile = start;
+        int b = uniform(find_seq(prefix, a.d.batch, tile));
+        while (tile < end) {
+            while (prefix[b + 1] <= tile) ++b;
+            b = uniform(b);
+            const int32_t seq0 = uniform(prefix[b]);
+            const int32_t seq1 = uniform(prefix[b + 1]);
+            const int32_t seg1 = min(end, seq1);
+            const int32_t t0 = tile - seq0, t1 = seg1 - seq0;
+            const bool whole = tile == seq0 && seg1 == seq1;
+            const int slot_index = 2 * w + (start >= seq0 ? 0 : 1);
+            int64_t slot;
+            const int64_t len = uniform64(seq_tokens(a.d, b, &slot));
+            slot = uniform64(slot);
+            const int32_t* table_row = a.d.block_table + slot * a.d.bt_width;
+
+            // Q^T operand of this head's G query heads (columns g >= G are zero).
+            bf16x8_t qh[2 * C], ql[2 * C];
+            const int hq = h * G + m16;
+            const bool qlive = m16 < G;
+#pragma unroll
+            for (int c = 0; c < C; ++c) {
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                    const int d0 = 64 * c + 16 * j + 8 * half;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        const float x = qlive ? load_q<QT>(a.d, b, hq, d0 + i) : 0.0f;
+                        const __bf16 hi = (__bf16)x;
+                        qh[2 * c + half][i] = hi;
+                        if constexpr (kHiLo) ql[2 * c + half][i] = (__bf16)(x - (float)hi);
+                    }
+                }
+            }
+
+            WaveState<C> st;
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) st.o[nb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            st.m = kNegInf;
+            st.l = 0.0f;
+
+            // Two-buffer pipeline: the loads of step T + 2 are in flight while
+            // step T is computed.
+            StepData<C> buf0, buf1;
+            int32_t T = t0;
+            TileRef ra = tile_ref(a, table_row, T);
+            TileRef rb = T + 1 < t1 ? tile_ref(a, table_row, T + 1) : TileRef{0, 0};
+            load_step<C>(buf0, a, h, ra, rb, lane);
+            while (true) {
+                const int64_t pos = (int64_t)T * 16;
+                int lim_a = ra.valid ? (int)max((int64_t)0, min((int64_t)16, len - pos)) : 0;
+                int lim_b = rb.valid ? (int)max((int64_t)0, min((int64_t)16, len - pos - 16)) : 0;
+                TileRef na{0, 0}, nb_{0, 0};
+                const bool more = T + 2 < t1;
+                if (more) {
+                    na = tile_ref(a, table_row, T + 2);
+                    nb_ = T + 3 < t1 ? tile_ref(a, table_row, T + 3) : TileRef{0, 0};
+                    load_step<C>(buf1, a, h, na, nb_, lane);
+                }
+                compute_step<C, kHiLo>(st, buf0, qh, ql, stage, lane, lim_a, lim_b, a.d.score_scale);
+                if (!more) break;
+                T += 2;
+                ra = na;
+                rb = nb_;
+                const int64_t pos1 = (int64_t)T * 16;
+                lim_a = ra.valid ? (int)max((int64_t)0, min((int64_t)16, len - pos1)) : 0;
+                lim_b = rb.valid ? (int)max((int64_t)0, min((int64_t)16, len - pos1 - 16)) : 0;
+                const bool more1 = T + 2 < t1;
+                if (more1) {
+                    na = tile_ref(a, table_row, T + 2);
+                    nb_ = T + 3 < t1 ? tile_ref(a, table_row, T + 3) : TileRef{0, 0};
+                    load_step<C>(buf0, a, h, na, nb_, lane);
+                }
+                compute_step<C, kHiLo>(st, buf1, qh, ql, stage, lane, lim_a, lim_b, a.d.score_scale);
+                if (!more1) break;
+                T += 2;
+                ra = na;
+                rb = nb_;
+            }
+
+            // Denominator: sum the four lane groups of each column.
+            float lt = st.l + __shfl_xor(st.l, 16);
+            lt += __shfl_xor(lt, 32);
+            if (qlive) {
+                if (whole) {
+                    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+#pragma unroll
+                    for (int jj = 0; jj < 4; ++jj) {
+#pragma unroll
+                        for (int nb = 0; nb < NB; ++nb)
+                            store_out<QT>(a.d, b, hq, NB * (4 * j + jj) + nb, lt > 0.0f ? st.o[nb][jj] * inv : 0.0f);
+                    }
+                } else {
+                    const int64_t pi = (int64_t)slot_index * a.d.num_q_heads + hq;
+                    float* acc = a.part_acc + pi * D;
+#pragma unroll
+                    for (int jj = 0; jj < 4; ++jj) {
+#pragma unroll
+                        for (int nb = 0; nb < NB; ++nb) acc[NB * (4 * j + jj) + nb] = st.o[nb][jj];
+                    }
+                    if (j == 0) {
+                        a.part_m[pi] = st.m;
+                        a.part_l[pi] = lt;
+                    }
+                }
+            }
+            tile = seg1;
+        }
+    }
+}
+
+// Workgroup whose tile range holds tile x: the largest w with w W / groups <= x.
+__device__ __forceinline__ int32_t group_of(int64_t x, int64_t total, int64_t groups) {
+    return (int32_t)(((x + 1) * groups - 1) / total);
+}
+
+// Merge of the pieces of every cut sequence (reference decode_attention.py:437-550):
+//   M = max m_i; den = sum 2^(m_i - M) l_i; num = sum 2^(m_i - M) acc_i;
+//   out = den > 0 ? num / den : 0. Empty sequences get zeros.
+template <int QT>
+__global__ void __launch_bounds__(256)
+combine_mfma_kernel(MfmaArgs a) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t pair = (int64_t)blockIdx.x * 4 + wave;
+    if (pair >= (int64_t)a.d.batch * a.d.num_q_heads) return;
+    const int b = (int)(pair / a.d.num_q_heads);
+    const int hq = (int)(pair - (int64_t)b * a.d.num_q_heads);
+    const int D = a.d.head_dim;
+    const int32_t t0 = a.plan[b], t1 = a.plan[b + 1];
+    if (t1 == t0) {
+        for (int d = lane; d < D; d += 64) store_out<QT>(a.d, b, hq, d, 0.0f);
+        return;
+    }
+    const int64_t total = a.plan[a.d.batch];
+    const int64_t groups = a.plan[a.d.batch + 1];
+    const int32_t w0 = group_of(t0, total, groups), w1 = group_of(t1 - 1, total, groups);
+    if (w0 == w1) return;    // finished by the decode kernel
+    float M = kNegInf;
+    for (int32_t w = w0; w <= w1; ++w) {
+        const int64_t start = (int64_t)w * total / groups;
+        const int64_t pi = (int64_t)(2 * w + (start >= t0 ? 0 : 1)) * a.d.num_q_heads + hq;
+        M = fmaxf(M, a.part_m[pi]);
+    }
+    for (int d = lane; d < D; d += 64) {
+        float num = 0.0f, den = 0.0f;
+        for (int32_t w = w0; w <= w1; ++w) {
+            const int64_t start = (int64_t)w * total / groups;
+            const int64_t pi = (int64_t)(2 * w + (start >= t0 ? 0 : 1)) * a.d.num_q_heads + hq;
+            const float wgt = M == kNegInf ? 0.0f : exp2f(a.part_m[pi] - M);
+            den += wgt * a.part_l[pi];
+            num += wgt * a.part_acc[pi * D + d];
+        }
+        store_out<QT>(a.d, b, hq, d, den > 0.0f ? num / den : 0.0f);
+    }
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+int ilog2(int64_t x) {
+    int s = 0;
+    while ((int64_t)1 << s < x) ++s;
+    return s;
+}
+
+int waves_for(int32_t num_kv_heads) { return num_kv_heads < kMaxWaves ? num_kv_heads : kMaxWaves; }
+
+// Compute units of the current device (cached per device id).
+int device_cus() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
+int64_t max_groups(int32_t num_kv_heads) {
+    const int per_cu = kWavesPerCu / waves_for(num_kv_heads);
+    return (int64_t)device_cus() * (per_cu > 0 ? per_cu : 1);
+}
+
+template <int C, int QT>
+hipError_t launch_c(const MfmaArgs& a, int64_t cap, hipStream_t s, void (*before)(hipStream_t),
+                    void (*after)(hipStream_t)) {
+    const int threads = 64 * waves_for(a.d.num_kv_heads);
+    const size_t lds = (size_t)(a.d.batch + 1) * sizeof(int32_t);
+    const void* fn = reinterpret_cast<const void*>(&decode_mfma_kernel<C, QT>);
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, lds) != hipSuccess || per_cu <= 0)
+        per_cu = 1;
+    int64_t groups = (int64_t)device_cus() * per_cu;
+    groups = groups < cap ? groups : cap;
+    before(s);
+    hipLaunchKernelGGL((decode_mfma_kernel<C, QT>), dim3((unsigned)groups), dim3(threads), lds, s, a);
+    after(s);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    const int64_t pairs = (int64_t)a.d.batch * a.d.num_q_heads;
+    hipLaunchKernelGGL((combine_mfma_kernel<QT>), dim3((unsigned)((pairs + 3) / 4)), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool mfma_decode_supported(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                           int64_t bt_width, int32_t block_size, int kv_dtype) {
+    if (kv_dtype != KVFP8_E4M3FN) return false;
+    if (head_dim != 64 && head_dim != 128) return false;
+    if (block_size < 16 || block_size % 16 != 0) return false;
+    if (num_q_heads % num_kv_heads != 0 || num_q_heads / num_kv_heads > 16) return false;
+    if (num_kv_heads > kMaxWaves && num_kv_heads % kMaxWaves != 0) return false;
+    if (batch <= 0 || batch > kMfmaMaxBatch) return false;
+    // Tile indices are int32.
+    if ((int64_t)batch * bt_width * (block_size / 16) >= ((int64_t)1 << 31)) return false;
+    return true;
+}
+
+}  // namespace kvfp8
+
+namespace kvfp8 {
+
+// Workspace layout of the MFMA path: plan [batch + 2] int32, part_m, part_l
+// [2 G_max Hq] float, part_acc [2 G_max Hq D] float (each 256-byte aligned).
+int64_t mfma_workspace_layout(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                              int64_t offsets[4]) {
+    const int64_t states = 2 * max_groups(num_kv_heads) * num_q_heads;
+    int64_t off = 0;
+    offsets[0] = off;
+    off += (int64_t)align256((size_t)(batch + 2) * sizeof(int32_t));
+    offsets[1] = off;
+    off += (int64_t)align256((size_t)states * sizeof(float));
+    offsets[2] = off;
+    off += (int64_t)align256((size_t)states * sizeof(float));
+    offsets[3] = off;
+    off += (int64_t)align256((size_t)states * head_dim * sizeof(float));
+    return off;
+}
 
 template <int QT>
-hipError_t launch_mfma_decode(const DecodeArgs&, int64_t, hipStream_t) { return hipErrorNotSupported; }
+hipError_t launch_mfma_decode(const DecodeArgs& d, void* workspace, hipStream_t stream,
+                              void (*before)(hipStream_t), void (*after)(hipStream_t)) {
+    int64_t off[4];
+    mfma_workspace_layout(d.batch, d.num_q_heads, d.num_kv_heads, d.head_dim, off);
+    char* ws = reinterpret_cast<char*>(workspace);
+    MfmaArgs a;
+    a.d = d;
+    a.tps_shift = ilog2(d.block_size / 16);
+    a.plan = reinterpret_cast<int32_t*>(ws + off[0]);
+    a.part_m = reinterpret_cast<float*>(ws + off[1]);
+    a.part_l = reinterpret_cast<float*>(ws + off[2]);
+    a.part_acc = reinterpret_cast<float*>(ws + off[3]);
+    const int64_t cap = max_groups(d.num_kv_heads);
+    if (d.head_dim == 64) return launch_c<1, QT>(a, cap, stream, before, after);
+    return launch_c<2, QT>(a, cap, stream, before, after);
+}
 
-template hipError_t launch_mfma_decode<KVFP8_F32>(const DecodeArgs&, int64_t, hipStream_t);
-template hipError_t launch_mfma_decode<KVFP8_F16>(const DecodeArgs&, int64_t, hipStream_t);
-template hipError_t launch_mfma_decode<KVFP8_BF16>(const DecodeArgs&, int64_t, hipStream_t);
+template hipError_t launch_mfma_decode<KVFP8_F32>(const DecodeArgs&, void*, hipStream_t, void (*)(hipStream_t),
+                                                  void (*)(hipStream_t));
+template hipError_t launch_mfma_decode<KVFP8_F16>(const DecodeArgs&, void*, hipStream_t, void (*)(hipStream_t),
+                                                  void (*)(hipStream_t));
+template hipError_t launch_mfma_decode<KVFP8_BF16>(const DecodeArgs&, void*, hipStream_t, void (*)(hipStream_t),
+                                                   void (*)(hipStream_t));
 
 }  // namespace kvfp8
