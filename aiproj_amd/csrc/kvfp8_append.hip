@@ -88,6 +88,9 @@ quantize_append_kernel(AppendArgs a) {
     const int D = a.head_dim;
     const int d0 = lane_in_row * kElemsPerLane;
 
+    // Page indices first: their latency overlaps the row load and the math.
+    const int64_t block = load_index(a.blocks, a.blocks64, t);
+    const int64_t offset = load_index(a.offsets, a.offsets64, t);
     const T* src = reinterpret_cast<const T*>(is_v ? a.v : a.k) +
                    t * (is_v ? a.v_stride_t : a.k_stride_t) + h * (is_v ? a.v_stride_h : a.k_stride_h);
     float x[kElemsPerLane];
@@ -104,8 +107,6 @@ quantize_append_kernel(AppendArgs a) {
 #pragma unroll
     for (int i = 0; i < kElemsPerLane; ++i) codes[i] = quantize_value(x[i], scale);
 
-    const int64_t block = load_index(a.blocks, a.blocks64, t);
-    const int64_t offset = load_index(a.offsets, a.offsets64, t);
     if (!live || block < 0 || block >= a.num_blocks || offset < 0 || offset >= a.block_size) return;
 
     const int64_t slot = (block * a.block_size + offset) * a.num_kv_heads + h;

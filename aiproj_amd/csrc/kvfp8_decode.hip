@@ -250,13 +250,10 @@ hipError_t launch_generic(const DecodeArgs& a, int64_t units_total, hipStream_t 
     int64_t blocks = (units_total + kWavesPerBlock - 1) / kWavesPerBlock;
     blocks = blocks < 1 ? 1 : (blocks > kMaxGrid ? kMaxGrid : blocks);
     const dim3 grid((unsigned)blocks), block(kDecodeThreads);
-    if (a.head_dim <= 128)
-        hipLaunchKernelGGL((decode_split_generic<KVT, QT, 32>), grid, block, lds, s, a);
-    else if (a.head_dim <= 256)
-        hipLaunchKernelGGL((decode_split_generic<KVT, QT, 64>), grid, block, lds, s, a);
-    else
-        hipLaunchKernelGGL((decode_split_generic<KVT, QT, 128>), grid, block, lds, s, a);
-    return hipGetLastError();
+    const KernelTiming timing = next_kernel_timing();
+    if (a.head_dim <= 128) return launch_timed(decode_split_generic<KVT, QT, 32>, grid, block, lds, s, timing, a);
+    if (a.head_dim <= 256) return launch_timed(decode_split_generic<KVT, QT, 64>, grid, block, lds, s, timing, a);
+    return launch_timed(decode_split_generic<KVT, QT, 128>, grid, block, lds, s, timing, a);
 }
 
 template <int QT>
@@ -267,36 +264,36 @@ hipError_t launch_combine(const DecodeArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-// Event pairs around split-kernel launches, armed by kvfp8_timing_enable.
-struct SplitTiming {
+// Event pairs of timed decode-kernel launches, armed by kvfp8_timing_enable.
+struct DecodeTiming {
     std::vector<hipEvent_t> start, stop;
     int32_t armed = 0;
     int32_t used = 0;
 };
-SplitTiming g_timing;
+DecodeTiming g_timing;
 
-void timing_before(hipStream_t s) {
-    if (g_timing.used < g_timing.armed) hipEventRecord(g_timing.start[g_timing.used], s);
+}  // namespace
+
+KernelTiming kvfp8::next_kernel_timing() {
+    if (g_timing.used >= g_timing.armed) return KernelTiming{nullptr, nullptr};
+    const int32_t i = g_timing.used++;
+    return KernelTiming{g_timing.start[i], g_timing.stop[i]};
 }
 
-void timing_after(hipStream_t s) {
-    if (g_timing.used < g_timing.armed) hipEventRecord(g_timing.stop[g_timing.used++], s);
-}
+namespace {
 
 template <int QT>
 hipError_t dispatch_kv(const DecodeArgs& a, int kv_dtype, const Plan& p, void* workspace, hipStream_t s) {
     const bool aligned = (((uintptr_t)a.k_cache | (uintptr_t)a.v_cache) & 15) == 0;
-    if (p.mfma && aligned) return launch_mfma_decode<QT>(a, workspace, s, timing_before, timing_after);
+    if (p.mfma && aligned) return launch_mfma_decode<QT>(a, workspace, s);
     const int64_t units_total = (int64_t)a.batch * p.max_chunks * a.num_q_heads;
     hipError_t err;
-    timing_before(s);
     switch (kv_dtype) {
         case KVFP8_E4M3FN: err = launch_generic<KVFP8_E4M3FN, QT>(a, units_total, s); break;
         case KVFP8_BF16: err = launch_generic<KVFP8_BF16, QT>(a, units_total, s); break;
         case KVFP8_F16: err = launch_generic<KVFP8_F16, QT>(a, units_total, s); break;
         default: err = launch_generic<KVFP8_F32, QT>(a, units_total, s); break;
     }
-    timing_after(s);
     if (err != hipSuccess) return err;
     return launch_combine<QT>(a, s);
 }

@@ -5,6 +5,8 @@
 
 #include "kvfp8_common.h"
 
+#include <hip/hip_ext.h>
+
 namespace kvfp8 {
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -117,6 +119,25 @@ template <int QT>
 __device__ __forceinline__ void store_out(const DecodeArgs& a, int b, int hq, int d, float x) {
     using T = typename Elem<QT>::T;
     reinterpret_cast<T*>(a.out)[((int64_t)b * a.num_q_heads + hq) * a.head_dim + d] = Elem<QT>::store(x);
+}
+
+// Start/stop events of the next timed decode-kernel launch; both null unless a
+// benchmark armed kvfp8_timing_enable. The events ride on the dispatch itself
+// (hipExtLaunchKernel), so they time the kernel and not the queue around it.
+struct KernelTiming {
+    hipEvent_t start;
+    hipEvent_t stop;
+};
+KernelTiming next_kernel_timing();
+
+template <typename Kernel, typename... Args>
+hipError_t launch_timed(Kernel kernel, dim3 grid, dim3 block, size_t lds, hipStream_t stream,
+                        const KernelTiming& timing, Args... args) {
+    if (timing.start != nullptr)
+        hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)lds, stream, timing.start, timing.stop, 0u, args...);
+    else
+        hipLaunchKernelGGL(kernel, grid, block, lds, stream, args...);
+    return hipGetLastError();
 }
 
 }  // namespace kvfp8

@@ -16,7 +16,6 @@ int64_t mfma_workspace_layout(int32_t batch, int32_t num_q_heads, int32_t num_kv
                               int64_t offsets[4]);
 
 template <int QT>
-hipError_t launch_mfma_decode(const DecodeArgs& a, void* workspace, hipStream_t stream,
-                              void (*before)(hipStream_t), void (*after)(hipStream_t));
+hipError_t launch_mfma_decode(const DecodeArgs& a, void* workspace, hipStream_t stream);
 
 }  // namespace kvfp8

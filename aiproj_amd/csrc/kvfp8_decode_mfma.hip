@@ -46,6 +46,8 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kMaxWaves = 8;            // KV heads served by one workgroup at a time
 constexpr int kMaxThreads = 64 * kMaxWaves;
@@ -96,8 +98,10 @@ __device__ __forceinline__ f32x4_t mma(bf16x8_t a, bf16x8_t b, f32x4_t c) {
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Tile prefix over the batch in LDS: prefix[b] = sum_{i<b} ceil(len_i / 16).
-__device__ void build_tile_prefix(const DecodeArgs& a, int32_t* prefix, int32_t* scan) {
+// Per-thread runs, a shuffle scan inside each wave, then the wave totals.
+__device__ void build_tile_prefix(const DecodeArgs& a, int32_t* prefix, int32_t* wave_total) {
     const int threads = blockDim.x, tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
     const int per = (a.batch + threads - 1) / threads;
     const int begin = tid * per;
     int32_t local = 0;
@@ -109,20 +113,21 @@ __device__ void build_tile_prefix(const DecodeArgs& a, int32_t* prefix, int32_t*
             local += (int32_t)((seq_tokens(a, b, &slot) + 15) >> 4);
         }
     }
-    scan[tid] = local;
-    __syncthreads();
-    for (int off = 1; off < threads; off <<= 1) {
-        const int32_t add = tid >= off ? scan[tid - off] : 0;
-        __syncthreads();
-        scan[tid] += add;
-        __syncthreads();
+    int32_t incl = local;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int32_t y = __shfl_up(incl, off);
+        if (lane >= off) incl += y;
     }
-    const int32_t base = tid > 0 ? scan[tid - 1] : 0;
+    if (lane == 63) wave_total[wave] = incl;
+    __syncthreads();
+    int32_t base = incl - local;
+    for (int w = 0; w < wave; ++w) base += wave_total[w];
     for (int i = 0; i < per; ++i) {
         const int b = begin + i;
         if (b < a.batch) prefix[b] += base;
     }
-    if (tid == threads - 1) prefix[a.batch] = scan[threads - 1];
+    if (tid == threads - 1) prefix[a.batch] = base + local;
     __syncthreads();
 }
 
@@ -147,8 +152,8 @@ __device__ __forceinline__ TileRef tile_ref(const MfmaArgs& a, const int32_t* ta
 // Loads of one 32-token step of one KV head.
 template <int C>
 struct StepData {
-    uint4 ka[C];          // tile A: token (l % 16), bytes 64 c + 16 (l / 16) .. + 16
-    uint4 kb[C];          // tile B, same bytes
+    u32x4_t ka[C];        // tile A: token (l % 16), bytes 64 c + 16 (l / 16) .. + 16
+    u32x4_t kb[C];        // tile B, same bytes
     uint32_t v[8][C];     // rows i: token 4 (l/16) + (i % 4) of tile (i < 4 ? A : B), bytes 4C (l % 16) ..
     float sc;             // lane l: [k|v][tile A|B][token l % 16] scale
 };
@@ -166,18 +171,21 @@ __device__ __forceinline__ void load_step(StepData<C>& s, const MfmaArgs& a, int
     const uint8_t* kc = reinterpret_cast<const uint8_t*>(a.d.k_cache);
     const uint8_t* vc = reinterpret_cast<const uint8_t*>(a.d.v_cache);
     const uint32_t koff = (uint32_t)(m16 * row_stride + 16 * j);
+    // K rows are read as two 64-byte halves by two instructions (normal loads
+    // keep the line in L2 between them); every V instruction reads whole
+    // 128-byte rows, streamed with nontemporal loads.
 #pragma unroll
     for (int c = 0; c < C; ++c) {
-        s.ka[c] = *reinterpret_cast<const uint4*>(kc + ea + koff + 64 * c);
-        s.kb[c] = *reinterpret_cast<const uint4*>(kc + eb + koff + 64 * c);
+        s.ka[c] = *reinterpret_cast<const u32x4_t*>(kc + ea + koff + 64 * c);
+        s.kb[c] = *reinterpret_cast<const u32x4_t*>(kc + eb + koff + 64 * c);
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const uint8_t* p = vc + (i < 4 ? ea : eb) + (uint32_t)((4 * j + (i & 3)) * row_stride + NB * m16);
         if constexpr (C == 1) {
-            s.v[i][0] = *reinterpret_cast<const uint32_t*>(p);
+            s.v[i][0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
         } else {
-            const uint2 x = *reinterpret_cast<const uint2*>(p);
+            const u32x2_t x = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p));
             s.v[i][0] = x.x;
             s.v[i][1] = x.y;
         }
@@ -216,10 +224,8 @@ __device__ __forceinline__ void compute_step(WaveState<C>& st, const StepData<C>
     for (int c = 0; c < C; ++c) {
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
-            const uint32_t* wa = reinterpret_cast<const uint32_t*>(&s.ka[c]);
-            const uint32_t* wb = reinterpret_cast<const uint32_t*>(&s.kb[c]);
-            const bf16x8_t ka = fp8x8(wa[2 * half], wa[2 * half + 1]);
-            const bf16x8_t kb = fp8x8(wb[2 * half], wb[2 * half + 1]);
+            const bf16x8_t ka = fp8x8(s.ka[c][2 * half], s.ka[c][2 * half + 1]);
+            const bf16x8_t kb = fp8x8(s.kb[c][2 * half], s.kb[c][2 * half + 1]);
             sa = mma(ka, qh[2 * c + half], sa);
             sb = mma(kb, qh[2 * c + half], sb);
             if constexpr (kHiLo) {
@@ -311,10 +317,10 @@ decode_mfma_kernel(MfmaArgs a) {
     constexpr int NB = 4 * C;
     constexpr bool kHiLo = QT != KVFP8_BF16;
     extern __shared__ int32_t prefix[];                // [batch + 1]
-    __shared__ int32_t scan[kMaxThreads];
+    __shared__ int32_t wave_total[kMaxWaves];
     __shared__ float4 stage_all[kMaxWaves][16];
 
-    build_tile_prefix(a.d, prefix, scan);
+    build_tile_prefix(a.d, prefix, wave_total);
     const int32_t total = prefix[a.d.batch];
     const int32_t want = (total + kMinTilesPerGroup - 1) / kMinTilesPerGroup;
     const int32_t groups = min((int32_t)gridDim.x, max(want, 1));
@@ -350,7 +356,22 @@ decode_mfma_kernel(MfmaArgs a) {
             slot = uniform64(slot);
             const int32_t* table_row = a.d.block_table + slot * a.d.bt_width;
 
-            // Q^T operand of this head's G query heads (columns g >= G are zero).
+            WaveState<C> st;
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) st.o[nb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            st.m = kNegInf;
+            st.l = 0.0f;
+
+            // Two-buffer pipeline: the loads of step T + 2 are in flight while
+            // step T is computed.
+            StepData<C> buf0, buf1;
+            int32_t T = t0;
+            TileRef ra = tile_ref(a, table_row, T);
+            TileRef rb = T + 1 < t1 ? tile_ref(a, table_row, T + 1) : TileRef{0, 0};
+            load_step<C>(buf0, a, h, ra, rb, lane);
+
+            // Q^T operand of this head's G query heads (columns g >= G are zero),
+            // loaded while the first KV step is in flight.
             bf16x8_t qh[2 * C], ql[2 * C];
             const int hq = h * G + m16;
             const bool qlive = m16 < G;
@@ -369,19 +390,6 @@ decode_mfma_kernel(MfmaArgs a) {
                 }
             }
 
-            WaveState<C> st;
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb) st.o[nb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-            st.m = kNegInf;
-            st.l = 0.0f;
-
-            // Two-buffer pipeline: the loads of step T + 2 are in flight while
-            // step T is computed.
-            StepData<C> buf0, buf1;
-            int32_t T = t0;
-            TileRef ra = tile_ref(a, table_row, T);
-            TileRef rb = T + 1 < t1 ? tile_ref(a, table_row, T + 1) : TileRef{0, 0};
-            load_step<C>(buf0, a, h, ra, rb, lane);
             while (true) {
                 const int64_t pos = (int64_t)T * 16;
                 int lim_a = ra.valid ? (int)max((int64_t)0, min((int64_t)16, len - pos)) : 0;
@@ -453,40 +461,80 @@ __device__ __forceinline__ int32_t group_of(int64_t x, int64_t total, int64_t gr
 // Merge of the pieces of every cut sequence (reference decode_attention.py:437-550):
 //   M = max m_i; den = sum 2^(m_i - M) l_i; num = sum 2^(m_i - M) acc_i;
 //   out = den > 0 ? num / den : 0. Empty sequences get zeros.
-template <int QT>
+// One wave per (sequence, q head). Piece states are read lane-parallel (m and l
+// one piece per lane, acc as float4 runs with D/4 lanes per piece), so the merge
+// costs a couple of memory latencies whatever the number of pieces.
+template <int C, int QT>
 __global__ void __launch_bounds__(256)
 combine_mfma_kernel(MfmaArgs a) {
+    constexpr int D = 64 * C;
+    constexpr int kLanesPerPiece = D / 4;
+    constexpr int kPiecesPerPass = 64 / kLanesPerPiece;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t pair = (int64_t)blockIdx.x * 4 + wave;
     if (pair >= (int64_t)a.d.batch * a.d.num_q_heads) return;
     const int b = (int)(pair / a.d.num_q_heads);
     const int hq = (int)(pair - (int64_t)b * a.d.num_q_heads);
-    const int D = a.d.head_dim;
     const int32_t t0 = a.plan[b], t1 = a.plan[b + 1];
+    const int d4 = lane % kLanesPerPiece, po = lane / kLanesPerPiece;
     if (t1 == t0) {
-        for (int d = lane; d < D; d += 64) store_out<QT>(a.d, b, hq, d, 0.0f);
+        if (po == 0) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) store_out<QT>(a.d, b, hq, 4 * d4 + e, 0.0f);
+        }
         return;
     }
     const int64_t total = a.plan[a.d.batch];
     const int64_t groups = a.plan[a.d.batch + 1];
     const int32_t w0 = group_of(t0, total, groups), w1 = group_of(t1 - 1, total, groups);
     if (w0 == w1) return;    // finished by the decode kernel
-    float M = kNegInf;
-    for (int32_t w = w0; w <= w1; ++w) {
-        const int64_t start = (int64_t)w * total / groups;
-        const int64_t pi = (int64_t)(2 * w + (start >= t0 ? 0 : 1)) * a.d.num_q_heads + hq;
-        M = fmaxf(M, a.part_m[pi]);
+    const int32_t pieces = w1 - w0 + 1;
+    const int64_t hq_count = a.d.num_q_heads;
+    auto state_index = [&](int32_t i) -> int64_t {
+        const int64_t w = w0 + i;
+        const int64_t start = w * total / groups;
+        return (2 * w + (start >= t0 ? 0 : 1)) * hq_count + hq;
+    };
+
+    // Each lane merges its pieces online (all loads independent, issued
+    // together), then the lane groups merge pairwise through shuffles.
+    float mr = kNegInf, den = 0.0f;
+    float4 num = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll 4
+    for (int32_t i = po; i < pieces; i += kPiecesPerPass) {
+        const int64_t si = state_index(i);
+        const float mi = a.part_m[si];
+        const float li = a.part_l[si];
+        const float4 x = reinterpret_cast<const float4*>(a.part_acc + si * D)[d4];
+        const float mn = fmaxf(mr, mi);
+        const float mu = mn == kNegInf ? 0.0f : mn;
+        const float sa = fast_exp2(mr - mu), sb = fast_exp2(mi - mu);
+        num.x = num.x * sa + x.x * sb;
+        num.y = num.y * sa + x.y * sb;
+        num.z = num.z * sa + x.z * sb;
+        num.w = num.w * sa + x.w * sb;
+        den = den * sa + li * sb;
+        mr = mn;
     }
-    for (int d = lane; d < D; d += 64) {
-        float num = 0.0f, den = 0.0f;
-        for (int32_t w = w0; w <= w1; ++w) {
-            const int64_t start = (int64_t)w * total / groups;
-            const int64_t pi = (int64_t)(2 * w + (start >= t0 ? 0 : 1)) * a.d.num_q_heads + hq;
-            const float wgt = M == kNegInf ? 0.0f : exp2f(a.part_m[pi] - M);
-            den += wgt * a.part_l[pi];
-            num += wgt * a.part_acc[pi * D + d];
-        }
-        store_out<QT>(a.d, b, hq, d, den > 0.0f ? num / den : 0.0f);
+#pragma unroll
+    for (int off = kLanesPerPiece; off < 64; off <<= 1) {
+        const float mo = __shfl_xor(mr, off);
+        const float mn = fmaxf(mr, mo);
+        const float mu = mn == kNegInf ? 0.0f : mn;
+        const float sa = fast_exp2(mr - mu), sb = fast_exp2(mo - mu);
+        num.x = num.x * sa + __shfl_xor(num.x, off) * sb;
+        num.y = num.y * sa + __shfl_xor(num.y, off) * sb;
+        num.z = num.z * sa + __shfl_xor(num.z, off) * sb;
+        num.w = num.w * sa + __shfl_xor(num.w, off) * sb;
+        den = den * sa + __shfl_xor(den, off) * sb;
+        mr = mn;
+    }
+    if (po == 0) {
+        const bool ok = den > 0.0f;
+        store_out<QT>(a.d, b, hq, 4 * d4 + 0, ok ? num.x / den : 0.0f);
+        store_out<QT>(a.d, b, hq, 4 * d4 + 1, ok ? num.y / den : 0.0f);
+        store_out<QT>(a.d, b, hq, 4 * d4 + 2, ok ? num.z / den : 0.0f);
+        store_out<QT>(a.d, b, hq, 4 * d4 + 3, ok ? num.w / den : 0.0f);
     }
 }
 
@@ -519,23 +567,28 @@ int64_t max_groups(int32_t num_kv_heads) {
 }
 
 template <int C, int QT>
-hipError_t launch_c(const MfmaArgs& a, int64_t cap, hipStream_t s, void (*before)(hipStream_t),
-                    void (*after)(hipStream_t)) {
+hipError_t launch_c(const MfmaArgs& a, int64_t cap, hipStream_t s) {
     const int threads = 64 * waves_for(a.d.num_kv_heads);
     const size_t lds = (size_t)(a.d.batch + 1) * sizeof(int32_t);
-    const void* fn = reinterpret_cast<const void*>(&decode_mfma_kernel<C, QT>);
-    int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, lds) != hipSuccess || per_cu <= 0)
-        per_cu = 1;
+    // Resident workgroups per CU, queried once per (device, workgroup size); the
+    // dynamic LDS (<= 32 KiB) never limits residency at these sizes.
+    static int resident[64][kMaxWaves + 1] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    int& per_cu = resident[dev][threads / 64];
+    if (per_cu == 0) {
+        const void* fn = reinterpret_cast<const void*>(&decode_mfma_kernel<C, QT>);
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, threads, lds) != hipSuccess || n <= 0) n = 1;
+        per_cu = n;
+    }
     int64_t groups = (int64_t)device_cus() * per_cu;
     groups = groups < cap ? groups : cap;
-    before(s);
-    hipLaunchKernelGGL((decode_mfma_kernel<C, QT>), dim3((unsigned)groups), dim3(threads), lds, s, a);
-    after(s);
-    hipError_t err = hipGetLastError();
+    const hipError_t err = launch_timed(decode_mfma_kernel<C, QT>, dim3((unsigned)groups), dim3(threads), lds, s,
+                                        next_kernel_timing(), a);
     if (err != hipSuccess) return err;
     const int64_t pairs = (int64_t)a.d.batch * a.d.num_q_heads;
-    hipLaunchKernelGGL((combine_mfma_kernel<QT>), dim3((unsigned)((pairs + 3) / 4)), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((combine_mfma_kernel<C, QT>), dim3((unsigned)((pairs + 3) / 4)), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
@@ -576,8 +629,7 @@ int64_t mfma_workspace_layout(int32_t batch, int32_t num_q_heads, int32_t num_kv
 }
 
 template <int QT>
-hipError_t launch_mfma_decode(const DecodeArgs& d, void* workspace, hipStream_t stream,
-                              void (*before)(hipStream_t), void (*after)(hipStream_t)) {
+hipError_t launch_mfma_decode(const DecodeArgs& d, void* workspace, hipStream_t stream) {
     int64_t off[4];
     mfma_workspace_layout(d.batch, d.num_q_heads, d.num_kv_heads, d.head_dim, off);
     char* ws = reinterpret_cast<char*>(workspace);
@@ -589,15 +641,12 @@ hipError_t launch_mfma_decode(const DecodeArgs& d, void* workspace, hipStream_t 
     a.part_l = reinterpret_cast<float*>(ws + off[2]);
     a.part_acc = reinterpret_cast<float*>(ws + off[3]);
     const int64_t cap = max_groups(d.num_kv_heads);
-    if (d.head_dim == 64) return launch_c<1, QT>(a, cap, stream, before, after);
-    return launch_c<2, QT>(a, cap, stream, before, after);
+    if (d.head_dim == 64) return launch_c<1, QT>(a, cap, stream);
+    return launch_c<2, QT>(a, cap, stream);
 }
 
-template hipError_t launch_mfma_decode<KVFP8_F32>(const DecodeArgs&, void*, hipStream_t, void (*)(hipStream_t),
-                                                  void (*)(hipStream_t));
-template hipError_t launch_mfma_decode<KVFP8_F16>(const DecodeArgs&, void*, hipStream_t, void (*)(hipStream_t),
-                                                  void (*)(hipStream_t));
-template hipError_t launch_mfma_decode<KVFP8_BF16>(const DecodeArgs&, void*, hipStream_t, void (*)(hipStream_t),
-                                                   void (*)(hipStream_t));
+template hipError_t launch_mfma_decode<KVFP8_F32>(const DecodeArgs&, void*, hipStream_t);
+template hipError_t launch_mfma_decode<KVFP8_F16>(const DecodeArgs&, void*, hipStream_t);
+template hipError_t launch_mfma_decode<KVFP8_BF16>(const DecodeArgs&, void*, hipStream_t);
 
 }  // namespace kvfp8

@@ -85,9 +85,27 @@ class Setup:
         cache.append_kv(self.w.new_blocks, self.w.new_offsets, k, v)
         return decode_attention_wrapper(self.w.q, cache, self.context)
 
+    def capture(self):
+        """One HIP graph per pool holding that pool's whole step (append, decode,
+        combine), as a serving loop captures its decode step."""
+        import torch as t
+
+        graphs = []
+        for i in range(self.num_pools):
+            g = t.cuda.CUDAGraph()
+            with t.cuda.graph(g):
+                self.step(i)
+            graphs.append(g)
+        t.cuda.synchronize()
+        return graphs
+
 
 def time_steps(setup: Setup, steps: int, warmup: int):
-    """(ms per step, mean split-kernel ms) over `steps` timed steps after `warmup`."""
+    """Two timed regions of `steps` steps each, after `warmup` eager steps:
+      * graph replay of the step (no host work between steps): ms per step;
+      * eager steps with HIP events around every decode-kernel launch on its
+        stream: mean kernel ms, and the eager ms per step.
+    """
     import ctypes
     import torch as t
     from aiproj_amd import _native
@@ -96,19 +114,32 @@ def time_steps(setup: Setup, steps: int, warmup: int):
     for i in range(warmup):
         setup.step(i)
     t.cuda.synchronize()
-    _native.check(lib.kvfp8_timing_enable(steps), "kvfp8_timing_enable")
+    graphs = setup.capture()
+    for g in graphs:
+        g.replay()
+    t.cuda.synchronize()
     start, end = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        graphs[i % len(graphs)].replay()
+    end.record()
+    t.cuda.synchronize()
+    graph_ms = start.elapsed_time(end) / steps
+    del graphs
+
+    _native.check(lib.kvfp8_timing_enable(steps), "kvfp8_timing_enable")
     t.cuda.synchronize()
     start.record()
     for i in range(steps):
         setup.step(warmup + i)
     end.record()
     t.cuda.synchronize()
+    eager_ms = start.elapsed_time(end) / steps
     total_ms = ctypes.c_double(0.0)
     launches = ctypes.c_int64(0)
     _native.check(lib.kvfp8_timing_read(ctypes.byref(total_ms), ctypes.byref(launches)), "kvfp8_timing_read")
     kernel_ms = total_ms.value / max(1, launches.value)
-    return start.elapsed_time(end) / steps, kernel_ms, launches.value
+    return graph_ms, eager_ms, kernel_ms, launches.value
 
 
 def copy_bandwidth_gbs(nbytes: int = 2 * 2 ** 30) -> float:
@@ -188,22 +219,27 @@ def cpu_baseline(setup: Setup, budget_s: float):
 
 
 def traffic_for(kernel: str, workload: str):
-    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if measured."""
-    path = ROOT / "profiles" / f"{kernel}_{workload}_traffic.json"
+    """HBM bytes per launch of `kernel`, from the committed rocprofv3 FETCH_SIZE +
+    WRITE_SIZE summary of this workload (calibrated against a 2 GiB copy), or None."""
+    path = ROOT / "profiles" / f"{kernel}_{workload}_traffic.md"
     if not path.exists():
         return None
-    return json.loads(path.read_text()).get("hbm_bytes_per_launch")
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(float(line.split(":", 1)[1]))
+    return None
 
 
 def measure(name: str, steps: int, warmup: int):
     import torch as t
 
     setup = Setup(name, "cuda")
-    ms, kernel_ms, launches = time_steps(setup, steps, warmup)
+    ms, eager_ms, kernel_ms, launches = time_steps(setup, steps, warmup)
     s = setup.spec
     result = {
         "setup": setup,
         "ms_per_step": ms,
+        "eager_ms_per_step": eager_ms,
         "split_kernel_ms": kernel_ms,
         "timed_launches": launches,
         "step_bytes": setup.decode_bytes + setup.append_bytes,
@@ -214,9 +250,9 @@ def measure(name: str, steps: int, warmup: int):
         "pool_mb": setup.pool_bytes / 1e6,
     }
     log(f"[{name}] B={s.batch} Hq={s.num_q_heads} Hkv={s.num_kv_heads} D={s.head_dim} tokens={s.total_tokens} "
-        f"pools={setup.num_pools}x{setup.pool_bytes / 1e6:.0f}MB: {ms * 1e3:.1f} us/step, "
-        f"split kernel {kernel_ms * 1e3:.1f} us ({result['kernel_gbs']:.0f} GB/s), "
-        f"step {result['gbs']:.0f} GB/s")
+        f"pools={setup.num_pools}x{setup.pool_bytes / 1e6:.0f}MB: {ms * 1e3:.1f} us/step (graph), "
+        f"{eager_ms * 1e3:.1f} us/step (eager), decode kernel {kernel_ms * 1e3:.1f} us "
+        f"({result['kernel_gbs']:.0f} GB/s), step {result['gbs']:.0f} GB/s")
     t.cuda.synchronize()
     return result
 
@@ -253,8 +289,9 @@ def main():
             "pct_of_peak": round(100 * r["gbs"] / PEAK_HBM_GBS, 2),
             "kv_tokens_per_s": round(r["kv_tokens_per_s"]),
             "ms_per_step": round(r["ms_per_step"], 5),
-            "split_kernel_us": round(r["split_kernel_ms"] * 1e3, 2),
-            "split_kernel_gbs": round(r["kernel_gbs"], 1),
+            "eager_ms_per_step": round(r["eager_ms_per_step"], 5),
+            "decode_kernel_us": round(r["split_kernel_ms"] * 1e3, 2),
+            "decode_kernel_gbs": round(r["kernel_gbs"], 1),
         }
         del r
 
@@ -269,6 +306,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(main_result["ms_per_step"], 5),
+        "eager_ms_per_step": round(main_result["eager_ms_per_step"], 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -287,13 +325,13 @@ def main():
         "copy_gbs": round(copy_gbs, 1),
         "pct_of_copy": round(100 * main_result["gbs"] / copy_gbs, 2),
         "roofline": {
-            "kernel": "decode split kernel",
+            "kernel": "decode_mfma_kernel",
             "bound": "hbm",
             "achieved": round(kernel_gbs, 1),
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(kernel_gbs / PEAK_HBM_GBS, 4),
-            "traffic": traffic_for("decode_split", s.name),
+            "traffic": traffic_for("decode_mfma_kernel", s.name),
             "algorithmic_bytes_per_launch": main_result["setup"].decode_bytes,
             "mean_launch_us": round(main_result["split_kernel_ms"] * 1e3, 2),
         },

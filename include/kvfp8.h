@@ -127,10 +127,10 @@ int kvfp8_paged_decode(const void* q_dev, int q_dtype, int64_t q_stride_b, int64
 
 /*
  * Kernel timing hook for benchmarks (not part of the reference interface).
- * kvfp8_timing_enable(n) arms HIP event pairs around the next n launches of the
- * decode split kernel (on the stream each launch uses); kvfp8_timing_read()
- * waits for those events and returns the summed kernel milliseconds and the
- * number of timed launches, then disarms. n <= 0 disarms.
+ * kvfp8_timing_enable(n) arms start/stop HIP events on the dispatch packets of
+ * the next n decode-kernel launches (hipExtLaunchKernel, on the stream each launch
+ * uses); kvfp8_timing_read() waits for those events and returns the summed kernel
+ * milliseconds and the number of timed launches, then disarms. n <= 0 disarms.
  */
 int kvfp8_timing_enable(int32_t max_launches);
 int kvfp8_timing_read(double* total_ms, int64_t* launches);

@@ -310,3 +310,34 @@ def test_decode_split_invariance():
                            context.cache_slots[row:row + 1], context.context_lengths[row:row + 1], 16)
         alone = decode_attention_wrapper(q[row:row + 1], read)
         t.testing.assert_close(alone[0].float(), batch[row].float(), rtol=1e-2, atol=4e-3)
+
+
+@t.inference_mode(False)
+def test_graph_capture_replays_match_eager():
+    # The decode step (append + decode + combine) captured once in a HIP graph and
+    # replayed several times, with eager work and synchronizations in between,
+    # gives the eager bits on every replay.
+    lengths = [2500, 40, 900, 1, 333]
+    cache = PagedKVCache(sum(-(-n // 16) for n in lengths) + 8, 16, 8, 128, "cuda", FP8)
+    manager, context, _, _ = fill_decode_batch([cache], lengths, 8, 128, 16, t.bfloat16, seed=13)
+    q = t.randn(len(lengths), 32, 128, device="cuda", dtype=t.bfloat16)
+    blocks = context.physical_blocks[:len(lengths)].clone()
+    offsets = context.block_offsets[:len(lengths)].clone()
+    new_k = t.randn(len(lengths), 8, 128, device="cuda", dtype=t.bfloat16)
+    new_v = t.randn_like(new_k)
+
+    def step():
+        cache.append_kv(blocks, offsets, new_k, new_v)
+        return decode_attention_wrapper(q, cache, context)
+
+    eager = step().clone()
+    t.cuda.synchronize()
+    graph = t.cuda.CUDAGraph()
+    with t.cuda.graph(graph):
+        out = step()
+    for _ in range(4):
+        cache.k.view(t.uint8)[blocks, offsets] = 0       # eager work the replay must undo
+        graph.replay()
+        t.cuda.synchronize()
+        assert t.equal(out, eager)
+        assert t.equal(eager, step())
