@@ -43,23 +43,19 @@ KVFP8_HD uint8_t encode_e4m3fn(float x) {
     const uint32_t bits = f32_bits(x);
     const uint32_t sign = (bits >> 24) & 0x80u;
     const uint32_t mag = bits & 0x7FFFFFFFu;
-    uint32_t code;
-    if (mag >= 0x7F800000u) {
-        code = 0x7Fu;                                  // inf or NaN
-    } else if (mag >= 0x3C800000u) {                   // |x| >= 2^-6: normal e4m3
-        // Keep the top 3 of 23 mantissa bits; round the 20 dropped bits half to
-        // even. A mantissa carry runs into the exponent field (the next code).
-        const uint32_t exponent = (mag >> 23) - 127u + 7u;
-        const uint32_t kept = (mag >> 20) & 0x7u;
-        const uint32_t dropped = mag & 0xFFFFFu;
-        const uint32_t up = (dropped > 0x80000u) | ((dropped == 0x80000u) & kept);
-        code = (exponent << 3) + kept + up;
-        if (code > 0x7Eu) code = 0x7Fu;                // rounds past 448: NaN
-    } else {
-        // Subnormal range: an integer number of 2^-9 steps. Scaling by 2^9 is
-        // exact and rintf rounds half to even; 8 steps is code 0x08 = 2^-6.
-        code = (uint32_t)rintf(bits_f32(mag) * 512.0f);
-    }
+    // |x| >= 2^-6 (normal e4m3): keep the top 3 of 23 mantissa bits and round
+    // the 20 dropped bits half to even; a mantissa carry runs into the exponent
+    // field, which is the next code. (Garbage below 2^-6, where it is not used.)
+    const uint32_t kept = (mag >> 20) & 0x7u;
+    const uint32_t dropped = mag & 0xFFFFFu;
+    const uint32_t up = (dropped > 0x80000u) | ((dropped == 0x80000u) & kept);
+    const uint32_t normal = ((mag >> 23) - 120u) * 8u + kept + up;
+    // |x| < 2^-6: an integer number of 2^-9 steps; scaling by 2^9 is exact and
+    // rintf rounds half to even; 8 steps is code 0x08 = 2^-6.
+    const uint32_t subnormal = (uint32_t)rintf(bits_f32(mag < 0x3C800000u ? mag : 0u) * 512.0f);
+    uint32_t code = mag >= 0x3C800000u ? normal : subnormal;
+    // Rounds past 448 (0x7E), or inf/NaN input: NaN (e4m3fn has no infinity).
+    code = (code > 0x7Eu || mag >= 0x7F800000u) ? 0x7Fu : code;
     return (uint8_t)(code | sign);
 }
 

@@ -362,16 +362,21 @@ decode_mfma_kernel(MfmaArgs a) {
             st.m = kNegInf;
             st.l = 0.0f;
 
-            // Two-buffer pipeline: the loads of step T + 2 are in flight while
-            // step T is computed.
-            StepData<C> buf0, buf1;
+            // Three-buffer pipeline: the loads of steps T + 2 and T + 4 are in
+            // flight while step T is computed.
+            StepData<C> buf0, buf1, buf2;
+            TileRef r0a, r0b, r1a, r1b, r2a, r2b;
+            auto issue = [&](StepData<C>& dst, int32_t tile0, TileRef& ra, TileRef& rb) {
+                ra = tile_ref(a, table_row, tile0);
+                rb = tile0 + 1 < t1 ? tile_ref(a, table_row, tile0 + 1) : TileRef{0, 0};
+                load_step<C>(dst, a, h, ra, rb, lane);
+            };
             int32_t T = t0;
-            TileRef ra = tile_ref(a, table_row, T);
-            TileRef rb = T + 1 < t1 ? tile_ref(a, table_row, T + 1) : TileRef{0, 0};
-            load_step<C>(buf0, a, h, ra, rb, lane);
+            issue(buf0, T, r0a, r0b);
+            if (T + 2 < t1) issue(buf1, T + 2, r1a, r1b);
 
             // Q^T operand of this head's G query heads (columns g >= G are zero),
-            // loaded while the first KV step is in flight.
+            // loaded while the first KV steps are in flight.
             bf16x8_t qh[2 * C], ql[2 * C];
             const int hq = h * G + m16;
             const bool qlive = m16 < G;
@@ -390,36 +395,25 @@ decode_mfma_kernel(MfmaArgs a) {
                 }
             }
 
+            auto compute = [&](const StepData<C>& cur, int32_t tile0, const TileRef& ra, const TileRef& rb) {
+                const int64_t pos = (int64_t)tile0 * 16;
+                const int lim_a = ra.valid ? (int)max((int64_t)0, min((int64_t)16, len - pos)) : 0;
+                const int lim_b = rb.valid ? (int)max((int64_t)0, min((int64_t)16, len - pos - 16)) : 0;
+                compute_step<C, kHiLo>(st, cur, qh, ql, stage, lane, lim_a, lim_b, a.d.score_scale);
+            };
             while (true) {
-                const int64_t pos = (int64_t)T * 16;
-                int lim_a = ra.valid ? (int)max((int64_t)0, min((int64_t)16, len - pos)) : 0;
-                int lim_b = rb.valid ? (int)max((int64_t)0, min((int64_t)16, len - pos - 16)) : 0;
-                TileRef na{0, 0}, nb_{0, 0};
-                const bool more = T + 2 < t1;
-                if (more) {
-                    na = tile_ref(a, table_row, T + 2);
-                    nb_ = T + 3 < t1 ? tile_ref(a, table_row, T + 3) : TileRef{0, 0};
-                    load_step<C>(buf1, a, h, na, nb_, lane);
-                }
-                compute_step<C, kHiLo>(st, buf0, qh, ql, stage, lane, lim_a, lim_b, a.d.score_scale);
-                if (!more) break;
+                if (T + 4 < t1) issue(buf2, T + 4, r2a, r2b);
+                compute(buf0, T, r0a, r0b);
                 T += 2;
-                ra = na;
-                rb = nb_;
-                const int64_t pos1 = (int64_t)T * 16;
-                lim_a = ra.valid ? (int)max((int64_t)0, min((int64_t)16, len - pos1)) : 0;
-                lim_b = rb.valid ? (int)max((int64_t)0, min((int64_t)16, len - pos1 - 16)) : 0;
-                const bool more1 = T + 2 < t1;
-                if (more1) {
-                    na = tile_ref(a, table_row, T + 2);
-                    nb_ = T + 3 < t1 ? tile_ref(a, table_row, T + 3) : TileRef{0, 0};
-                    load_step<C>(buf0, a, h, na, nb_, lane);
-                }
-                compute_step<C, kHiLo>(st, buf1, qh, ql, stage, lane, lim_a, lim_b, a.d.score_scale);
-                if (!more1) break;
+                if (T >= t1) break;
+                if (T + 4 < t1) issue(buf0, T + 4, r0a, r0b);
+                compute(buf1, T, r1a, r1b);
                 T += 2;
-                ra = na;
-                rb = nb_;
+                if (T >= t1) break;
+                if (T + 4 < t1) issue(buf1, T + 4, r1a, r1b);
+                compute(buf2, T, r2a, r2b);
+                T += 2;
+                if (T >= t1) break;
             }
 
             // Denominator: sum the four lane groups of each column.

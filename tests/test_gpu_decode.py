@@ -341,3 +341,21 @@ def test_graph_capture_replays_match_eager():
         t.cuda.synchronize()
         assert t.equal(out, eager)
         assert t.equal(eager, step())
+
+
+@t.inference_mode()
+def test_back_to_back_calls_read_fresh_partial_states():
+    # Two calls with equal shapes reuse the same workspace block from the caching
+    # allocator; the second must merge its own partial states, never the first's.
+    lengths = [3000, 2000, 17, 1000]
+    cache = PagedKVCache(sum(-(-n // 16) for n in lengths) + 8, 16, 8, 128, "cuda", FP8)
+    manager, context, _, _ = fill_decode_batch([cache], lengths, 8, 128, 16, t.bfloat16, seed=14)
+    outs, qs = [], []
+    for i in range(3):
+        q = t.randn(len(lengths), 32, 128, device="cuda", dtype=t.bfloat16) * (1 + i)
+        qs.append(q)
+        outs.append(decode_attention_wrapper(q, cache, context))
+    for q, out in zip(qs, outs):
+        expected = oracle_decode(q, cache, manager.block_table, context.cache_slots, lengths)
+        t.testing.assert_close(out.double().cpu(), t.from_numpy(expected),
+                               rtol=OUTPUT_TOLERANCE[t.bfloat16], atol=OUTPUT_TOLERANCE[t.bfloat16])
