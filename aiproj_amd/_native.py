@@ -47,6 +47,8 @@ SIGNATURES = {
     "kvfp8_version": (ctypes.c_char_p, []),
     "kvfp8_host_encode_e4m3fn": (None, [_P, _P, _I64]),
     "kvfp8_host_quantize_rows": (None, [_P, _I64, _I32, _P, _P]),
+    "kvfp8_host_row_quotients": (None, [_P, _I64, _I32, _P]),
+    "kvfp8_selftest_fp8_encoder": (_INT, [_P, _P]),
 }
 
 _lock = threading.Lock()

@@ -103,16 +103,35 @@ quantize_append_kernel(AppendArgs a) {
     for (int s = 1; s < LPR; s <<= 1) amax = max(amax, (uint32_t)__shfl_xor((int)amax, s, LPR));
 
     const float scale = row_scale(amax);
-    uint8_t codes[kElemsPerLane];
+    const RowDivider div(scale);
+    uint32_t packed[kElemsPerLane / 4];
+    if (div.fast && amax < 0x7F800000u) {
+        // Finite row, scale in the corrected-division range: |x / scale| <=
+        // 448 (1 + 2^-23), which needs no clamp and is never NaN, so the
+        // hardware round-to-nearest-even converter gives the oracle's codes
+        // (checked over every such float32 by kvfp8_selftest_fp8_encoder).
 #pragma unroll
-    for (int i = 0; i < kElemsPerLane; ++i) codes[i] = quantize_value(x[i], scale);
+        for (int i = 0; i < kElemsPerLane / 4; ++i) {
+            int w = __builtin_amdgcn_cvt_pk_fp8_f32(div.corrected(x[4 * i]), div.corrected(x[4 * i + 1]), 0, false);
+            w = __builtin_amdgcn_cvt_pk_fp8_f32(div.corrected(x[4 * i + 2]), div.corrected(x[4 * i + 3]), w, true);
+            packed[i] = (uint32_t)w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < kElemsPerLane / 4; ++i) {
+            packed[i] = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) packed[i] |= (uint32_t)clamp_encode(x[4 * i + e] / scale) << (8 * e);
+        }
+    }
+    const uint8_t* codes = reinterpret_cast<const uint8_t*>(packed);
 
     if (!live || block < 0 || block >= a.num_blocks || offset < 0 || offset >= a.block_size) return;
 
     const int64_t slot = (block * a.block_size + offset) * a.num_kv_heads + h;
     uint8_t* dst = reinterpret_cast<uint8_t*>(is_v ? a.v_cache : a.k_cache) + slot * D;
     if constexpr (VEC) {
-        if (d0 < D) *reinterpret_cast<uint4*>(dst + d0) = *reinterpret_cast<const uint4*>(codes);
+        if (d0 < D) *reinterpret_cast<uint4*>(dst + d0) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
     } else {
 #pragma unroll
         for (int i = 0; i < kElemsPerLane; ++i)
@@ -148,6 +167,21 @@ store_append_kernel(AppendArgs a, int lanes_per_row) {
         const int d = d0 + i;
         if (d < a.head_dim) dst[d] = Elem<DT_OUT>::store(Elem<DT_IN>::load(src[d]));
     }
+}
+
+// Every float32 bit pattern m with |x| <= 448 (1 + 2^-19) (sign from the grid's
+// y index): hardware converter vs the software encoder; counts mismatches.
+__global__ void __launch_bounds__(256) fp8_encoder_selftest_kernel(uint32_t limit, unsigned long long* mismatches) {
+    unsigned long long local = 0;
+    const uint32_t sign = blockIdx.y ? 0x80000000u : 0u;
+    for (uint32_t m = blockIdx.x * 256u + threadIdx.x; m <= limit; m += gridDim.x * 256u) {
+        const float a = bits_f32(m | sign);
+        const float b = bits_f32((limit - m) | sign);
+        const uint32_t hw = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+        local += (hw & 0xFFu) != encode_e4m3fn(a);
+        local += ((hw >> 8) & 0xFFu) != encode_e4m3fn(b);
+    }
+    if (local) atomicAdd(mismatches, local);
 }
 
 }  // namespace kvfp8
@@ -302,7 +336,26 @@ extern "C" void kvfp8_host_quantize_rows(const float* x, int64_t rows, int32_t h
         uint32_t amax = 0;
         for (int d = 0; d < head_dim; ++d) amax = amax > abs_bits(row[d]) ? amax : abs_bits(row[d]);
         const float scale = row_scale(amax);
+        const RowDivider div(scale);
         scales[r] = scale;
-        for (int d = 0; d < head_dim; ++d) codes[r * head_dim + d] = quantize_value(row[d], scale);
+        for (int d = 0; d < head_dim; ++d) codes[r * head_dim + d] = clamp_encode(div.divide(row[d]));
     }
+}
+
+extern "C" void kvfp8_host_row_quotients(const float* x, int64_t rows, int32_t head_dim, float* q) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const float* row = x + r * head_dim;
+        uint32_t amax = 0;
+        for (int d = 0; d < head_dim; ++d) amax = amax > abs_bits(row[d]) ? amax : abs_bits(row[d]);
+        const RowDivider div(row_scale(amax));
+        for (int d = 0; d < head_dim; ++d) q[r * head_dim + d] = div.divide(row[d]);
+    }
+}
+
+extern "C" int kvfp8_selftest_fp8_encoder(unsigned long long* mismatches_dev, void* stream) {
+    if (!mismatches_dev) return KVFP8_ENULL;
+    const uint32_t limit = 0x43E00010u;    // 448 (1 + 2^-19): every quotient the fast path makes
+    hipLaunchKernelGGL(fp8_encoder_selftest_kernel, dim3(8192, 2), dim3(256), 0,
+                       reinterpret_cast<hipStream_t>(stream), limit, mismatches_dev);
+    return (int)hipGetLastError();
 }

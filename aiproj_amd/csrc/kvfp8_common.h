@@ -134,12 +134,43 @@ KVFP8_HD float row_scale(uint32_t amax_bits) {
     return amax > 0.0f ? amax / kFp8Max : 1.0f;
 }
 
-// clamp(x / scale, -448, 448) keeping NaN (torch.clamp semantics), then RNE.
-KVFP8_HD uint8_t quantize_value(float x, float scale) {
-    float r = x / scale;
-    r = r > kFp8Max ? kFp8Max : r;
-    r = r < -kFp8Max ? -kFp8Max : r;
-    return encode_e4m3fn(r);
+// clamp(q, -448, 448) keeping NaN (torch.clamp semantics), then RNE.
+KVFP8_HD uint8_t clamp_encode(float q) {
+    q = q > kFp8Max ? kFp8Max : q;
+    q = q < -kFp8Max ? -kFp8Max : q;
+    return encode_e4m3fn(q);
 }
+
+// clamp(x / scale, -448, 448) then RNE, with IEEE division.
+KVFP8_HD uint8_t quantize_value(float x, float scale) { return clamp_encode(x / scale); }
+
+// x / scale for every element of a row that shares one scale, equal to the IEEE
+// float32 division. The reciprocal y = RN(1 / scale) is one correctly rounded
+// division per row; each quotient then costs a product and two FMA corrections:
+//   q0 = RN(x y),  q1 = RN(q0 + (x - scale q0) y),  q2 = RN(q1 + (x - scale q1) y).
+// The remainders x - scale q are exact with an FMA, q1 is within one ulp of
+// x / scale, and then the second correction gives RN(x / scale) (Markstein's
+// theorem). That needs normal intermediates: scale in [2^-60, 2^100] keeps the
+// remainders exact wherever |x / scale| >= 2^-11; smaller quotients round to a
+// zero code either way, and the sign is taken from x so -0 stays -0. Rows outside
+// that scale range (tiny, infinite or NaN scales) use the IEEE division.
+struct RowDivider {
+    float scale;
+    float recip;
+    bool fast;
+
+    KVFP8_HD explicit RowDivider(float s) : scale(s), recip(0.0f), fast(s >= 0x1p-60f && s <= 0x1p100f) {
+        if (fast) recip = 1.0f / s;
+    }
+
+    KVFP8_HD float corrected(float x) const {
+        const float q0 = x * recip;
+        const float q1 = fmaf(fmaf(-q0, scale, x), recip, q0);
+        const float q2 = fmaf(fmaf(-q1, scale, x), recip, q1);
+        return copysignf(q2, x);
+    }
+
+    KVFP8_HD float divide(float x) const { return fast ? corrected(x) : x / scale; }
+};
 
 }  // namespace kvfp8

@@ -149,6 +149,17 @@ const char* kvfp8_version(void);
 void kvfp8_host_encode_e4m3fn(const float* x, uint8_t* codes, int64_t n);
 void kvfp8_host_quantize_rows(const float* x, int64_t rows, int32_t head_dim,
                               uint8_t* codes, float* scales);
+/* x / scale of every element with its row's scale, by the device's division routine. */
+void kvfp8_host_row_quotients(const float* x, int64_t rows, int32_t head_dim, float* q);
+
+/*
+ * GPU self-test of the hardware float32 -> e4m3fn converter the append kernel uses
+ * for finite rows: adds to *mismatches_dev the number of float32 values with
+ * |x| <= 448 (1 + 2^-19) (both signs) whose hardware code differs from the
+ * software round-to-nearest-even encoder (which the CPU tests pin to the oracle).
+ * Not part of the reference interface.
+ */
+int kvfp8_selftest_fp8_encoder(unsigned long long* mismatches_dev, void* stream);
 
 #ifdef __cplusplus
 }

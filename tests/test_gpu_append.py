@@ -231,3 +231,15 @@ def test_golden_cfg1_cache_bytes():
     assert np.array_equal(kc, g["k_codes"]) and np.array_equal(vc, g["v_codes"])
     assert np.array_equal(ksc.view(np.uint32), g["k_scales"].view(np.uint32))
     assert np.array_equal(vsc.view(np.uint32), g["v_scales"].view(np.uint32))
+
+
+def test_hardware_encoder_matches_software_encoder_on_every_fast_path_value():
+    # The append kernel converts finite rows with the hardware RNE converter; it must
+    # agree with the software encoder (pinned to the oracle on the CPU) on every
+    # float32 the corrected division can produce, |x| <= 448 (1 + 2^-19), both signs.
+    from aiproj_amd import _native
+    mismatches = t.zeros(1, dtype=t.int64, device="cuda")
+    rc = _native.lib().kvfp8_selftest_fp8_encoder(mismatches.data_ptr(), _native.stream_handle(mismatches.device))
+    _native.check(rc, "kvfp8_selftest_fp8_encoder")
+    t.cuda.synchronize()
+    assert mismatches.item() == 0

@@ -118,3 +118,82 @@ def test_argument_errors_are_reported_before_any_launch(lib):
     # Empty batches are a no-op.
     assert lib.kvfp8_quantize_append(fake, fake, _native.BF16, 0, 0, 0, 0, fake, _native.I32, fake, _native.I32,
                                      0, 2, 64, 4, 16, fake, fake, fake, fake, None) == 0
+
+
+def _host_quotients(lib, x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    q = np.empty_like(x)
+    lib.kvfp8_host_row_quotients(x.ctypes.data, x.shape[0], x.shape[1], q.ctypes.data)
+    return q
+
+
+def _ieee_quotients(x: np.ndarray) -> np.ndarray:
+    with np.errstate(all="ignore"):
+        amax = np.abs(x).max(axis=-1)
+        scale = np.where(amax > 0, amax / np.float32(448.0), np.float32(1.0)).astype(np.float32)
+        return (x / scale[:, None]).astype(np.float32)
+
+
+def test_row_division_equals_ieee_division(lib):
+    # The device quotient routine (reciprocal + two FMA corrections) against IEEE
+    # float32 division, on rows whose magnitudes span the float32 range.
+    rng = np.random.default_rng(11)
+    rows, d = 40000, 128
+    exps = rng.integers(-60, 60, size=(rows, 1)).astype(np.float32)
+    x = (rng.standard_normal((rows, d)).astype(np.float32) * np.exp2(exps)).astype(np.float32)
+    x[::7, :5] = 0.0
+    x[::11, 3] *= np.float32(1e6)                 # outliers dominate the row's scale
+    got, want = _host_quotients(lib, x), _ieee_quotients(x)
+    same = got.view(np.uint32) == want.view(np.uint32)
+    big = np.abs(want) >= 2.0 ** -11
+    assert same[big].all(), f"{(~same[big]).sum()} quotients >= 2^-11 differ"
+    codes_got = oracle.f32_to_e4m3fn(np.clip(got, -448, 448))
+    codes_want = oracle.f32_to_e4m3fn(np.clip(want, -448, 448))
+    assert np.array_equal(codes_got, codes_want)
+
+
+def test_row_division_at_e4m3_rounding_ties(lib):
+    # Elements built as x = t * scale with t on e4m3 rounding ties and their float32
+    # neighbours: the quotient must land on the same side of every tie as IEEE.
+    rng = np.random.default_rng(12)
+    ties = np.array([m * 2.0 ** e for e in range(-9, 9) for m in (1.0625, 1.1875, 1.3125, 1.4375,
+                                                                   1.5625, 1.6875, 1.8125)], dtype=np.float32)
+    ties = ties[ties <= 448]
+    rows = []
+    for _ in range(3000):
+        amax = np.float32(rng.uniform(0.5, 2.0) * 2.0 ** rng.integers(-40, 40))
+        scale = np.float32(amax / np.float32(448.0))
+        t = rng.choice(ties, size=127)
+        base = (t * scale).astype(np.float32)
+        nudge = rng.integers(-2, 3, size=127).astype(np.int32)
+        xs = (base.view(np.int32) + nudge).view(np.float32)
+        rows.append(np.concatenate([[amax], xs * rng.choice([-1, 1], size=127).astype(np.float32)]))
+    x = np.stack(rows).astype(np.float32)
+    got, want = _host_quotients(lib, x), _ieee_quotients(x)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    codes = np.empty(x.shape, dtype=np.uint8)
+    scales = np.empty(x.shape[0], dtype=np.float32)
+    lib.kvfp8_host_quantize_rows(x.ctypes.data, x.shape[0], x.shape[1], codes.ctypes.data, scales.ctypes.data)
+    o_codes, o_scales = oracle.quantize(x)
+    assert np.array_equal(codes, o_codes) and np.array_equal(scales, o_scales)
+
+
+def test_row_division_special_rows_take_the_ieee_path(lib):
+    x = np.zeros((6, 64), dtype=np.float32)
+    x[0, 3] = np.inf                   # infinite scale
+    x[1, :] = 1e-38                    # scale below 2^-60
+    x[2, 5] = np.nan                   # NaN amax -> scale 1
+    x[3, :] = -0.0                     # zero row -> scale 1, codes keep the sign
+    x[4, :] = np.float32(3.0e38)       # huge but finite
+    x[5, :2] = [1e-45, -1e-45]         # subnormal inputs
+    codes = np.empty(x.shape, dtype=np.uint8)
+    scales = np.empty(x.shape[0], dtype=np.float32)
+    lib.kvfp8_host_quantize_rows(x.ctypes.data, x.shape[0], x.shape[1], codes.ctypes.data, scales.ctypes.data)
+    with np.errstate(all="ignore"):
+        o_codes, o_scales = oracle.quantize(x)
+    assert np.array_equal(codes, o_codes)
+    assert np.array_equal(scales.view(np.uint32), o_scales.view(np.uint32))
+
+
+def test_encoder_selftest_rejects_null(lib):
+    assert lib.kvfp8_selftest_fp8_encoder(None, None) == -4
