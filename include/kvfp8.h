@@ -126,6 +126,30 @@ int kvfp8_paged_decode(const void* q_dev, int q_dtype, int64_t q_stride_b, int64
                        void* stream);
 
 /*
+ * RMSNorm forward over rows of x [rows, d_model] (row stride x_stride elements):
+ *   inv_rms[r] = 1 / sqrt(mean_d x[r,d]^2 + eps); out[r,d] = (x[r,d] * inv_rms[r]) * weight[d]
+ * in float32, out stored in x's dtype (f32/f16/bf16); weight f32/f16/bf16; inv_rms
+ * (float32 [rows]) may be NULL.
+ * Replaces `triton_rmsnorm` + `rmsnorm_kernal`, reference
+ * src/torch_llm/model/rmsnorm.py:60-113.
+ */
+int kvfp8_rmsnorm_forward(const void* x_dev, int dtype, int64_t x_stride, int64_t rows, int32_t d_model,
+                          const void* weight_dev, int w_dtype, float eps,
+                          void* out_dev, int64_t out_stride, float* inv_rms_dev, void* stream);
+
+/*
+ * Residual add fused with the RMSNorm that follows it:
+ *   state_out = x + update (rounded to x's dtype), out = rmsnorm(state_out).
+ * Replaces `residual.write` + the next sublayer's norm, reference
+ * src/torch_llm/model/decoder_block.py:60-66 and model/residual.py:33-35.
+ */
+int kvfp8_add_rmsnorm_forward(const void* x_dev, const void* update_dev, int dtype,
+                              int64_t x_stride, int64_t update_stride, int64_t rows, int32_t d_model,
+                              const void* weight_dev, int w_dtype, float eps,
+                              void* state_out_dev, int64_t state_stride,
+                              void* out_dev, int64_t out_stride, float* inv_rms_dev, void* stream);
+
+/*
  * Kernel timing hook for benchmarks (not part of the reference interface).
  * kvfp8_timing_enable(n) arms start/stop HIP events on the dispatch packets of
  * the next n decode-kernel launches (hipExtLaunchKernel, on the stream each launch

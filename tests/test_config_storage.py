@@ -208,3 +208,13 @@ def test_resolve_batch_locations_expands_slots_per_token():
     assert offsets.tolist() == [0, 1, 1, 2, 2]
     with pytest.raises(ValueError):
         manager.resolve_batch_locations(t.tensor([a, b]), t.tensor([0, 3, 4], dtype=t.int32), positions)
+
+
+def test_rmsnorm_validates_on_the_host_and_refuses_cpu_tensors():
+    from aiproj_amd.model.rmsnorm import rmsnorm_forward
+    with pytest.raises(ValueError):
+        rmsnorm_forward(t.zeros(2, 3, 4), t.ones(4), 1e-5)
+    with pytest.raises(ValueError):
+        rmsnorm_forward(t.zeros(2, 4), t.ones(5), 1e-5)
+    with pytest.raises(RuntimeError):
+        rmsnorm_forward(t.zeros(2, 4), t.ones(4), 1e-5)
