@@ -1,0 +1,114 @@
+"""Prefill + greedy decode of a fixed batch, with a HIP-graph-capturable decode step.
+
+The counterpart of the reference runtime's prefill-then-decode loop
+(`src/torch_llm/inference/runtime.py:174-330`) for one fixed batch, reduced to
+what drives the FP8 paged KV-cache path:
+
+* `prefill(prompts)` reserves every sequence's whole lifetime in the
+  `PageAllocator` (reference full-lifetime reservation), runs the packed prompts
+  through the model (prompt attention, then the bulk quantized cache write) and
+  samples the first token (argmax at temperature 0, reference `sampling.py`);
+* `step()` is one decode step over the batch with no host synchronization: the
+  write locations `block_table[slot, pos // BS]`, `pos % BS` (reference
+  `page_allocator.py:225-245`), the context lengths (committed + 1, reference
+  `:347`) and the next positions are all computed on the device from buffers
+  that live as long as the decoder, so the step can be captured once in a HIP
+  graph and replayed (`capture()`, `generate()`).
+
+Unlike the reference runtime, the allocator's host-side lengths are advanced once
+after generation instead of every step (they are not read during it).
+"""
+
+from __future__ import annotations
+
+import torch as t
+
+from aiproj_amd.inference.page_allocator import CacheContainer, PageAllocator
+from aiproj_amd.inference.paged_kv_cache import PagedKVCache
+from aiproj_amd.model.transformer import StepMeta, TransformerLM
+
+
+class GreedyDecoder:
+    def __init__(self, model: TransformerLM, batch: int, max_len: int, cache_dtype=t.float8_e4m3fn,
+                 block_size: int = 16, device="cuda"):
+        cfg = model.cfg
+        self.model = model
+        self.batch = batch
+        self.block_size = block_size
+        self.max_len = max_len
+        pages = batch * (-(-max_len // block_size))
+        self.allocator = PageAllocator(pages, block_size, batch, max_len, device)
+        self.caches = [PagedKVCache(pages, block_size, cfg.num_kv_heads, cfg.head_dim, device, cache_dtype)
+                       for _ in range(cfg.num_layers)]
+        self.device = t.device(device)
+        self.slots = None
+        # Decode-step state, updated in place by every step (graph-stable addresses).
+        self.tokens = t.zeros(batch, dtype=t.int64, device=device)
+        self.positions = t.zeros(batch, dtype=t.int64, device=device)
+        self.context_lengths = t.zeros(batch, dtype=t.int32, device=device)
+        self.history = None
+        self.steps_left = 0
+        self.step_index = t.zeros(1, dtype=t.int64, device=device)
+        self.graph = None
+
+    def prefill(self, prompts: t.Tensor) -> t.Tensor:
+        """prompts [B, P] int64 -> first sampled tokens [B] (also the next step's input)."""
+        batch, length = prompts.shape
+        assert batch == self.batch and length < self.max_len
+        slots = [self.allocator.allocate_request(i, self.max_len) for i in range(batch)]
+        self.slots = t.tensor(slots, dtype=t.int64, device=self.device)
+        positions = t.arange(length, device=self.device).repeat(batch)
+        cu = t.arange(batch + 1, device=self.device, dtype=t.int32) * length
+        ctx = self.allocator.create_container(self.slots, cu, positions, validate=False)
+        meta = StepMeta("prefill", positions, ctx, seq_lens=[length] * batch)
+        logits = self.model(prompts.reshape(-1).to(self.device), meta, self.caches)
+        self.allocator.advance_batch(list(range(batch)), [length] * batch)
+        self.tokens.copy_(logits.argmax(-1))
+        self.positions.fill_(length)
+        self.context_lengths.fill_(length + 1)
+        # Every later token of every sequence, in decode order (fixed address).
+        self.history = t.zeros(self.max_len - length, batch, dtype=t.int64, device=self.device)
+        self.step_index.zero_()
+        self.steps_left = self.max_len - length
+        return self.tokens.clone()
+
+    def step(self) -> t.Tensor:
+        """One decode step: logits [B, vocab]; the argmax becomes the next input token.
+        Writes the new token's K/V at `positions`, so at most `max_len - prompt` steps."""
+        table = self.allocator.block_table
+        blocks = table[self.slots, self.positions // self.block_size]
+        offsets = self.positions % self.block_size
+        ctx = CacheContainer(self.slots, blocks, offsets, self.context_lengths, table)
+        meta = StepMeta("decode", self.positions, ctx)
+        logits = self.model(self.tokens, meta, self.caches)
+        nxt = logits.argmax(-1)
+        self.history.index_copy_(0, self.step_index, nxt.unsqueeze(0))
+        self.step_index.add_(1)
+        self.tokens.copy_(nxt)
+        self.positions.add_(1)
+        self.context_lengths.add_(1)
+        return logits
+
+    def capture(self):
+        """Capture one decode step in a HIP graph. Capture records without running,
+        so the decoder state is unchanged; every replay is one more step."""
+        self.graph = t.cuda.CUDAGraph()
+        with t.cuda.graph(self.graph):
+            self.logits = self.step()
+        return self.graph
+
+    def generate(self, steps: int, use_graph: bool = True) -> t.Tensor:
+        """`steps` decode steps -> their tokens [steps, B]. With `use_graph`, the first
+        step runs eagerly (warm-up), the step is captured, and the rest are replays."""
+        assert 0 < steps <= self.steps_left
+        start = int(self.step_index.item())
+        for i in range(steps):
+            if not use_graph:
+                self.step()
+            elif self.graph is None:
+                self.step()
+                self.capture()
+            else:
+                self.graph.replay()
+        self.steps_left -= steps
+        return self.history[start:start + steps]

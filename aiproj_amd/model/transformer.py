@@ -1,0 +1,200 @@
+"""Decoder LM that drives the FP8 paged KV-cache path end to end (config 5).
+
+Same block structure as the reference model (`src/torch_llm/model/model.py:48-77`,
+`decoder_block.py:41-69`, `attention.py:57-122`):
+
+    x = embed(tokens)
+    per layer: x = x + o_proj(attn(rope(q), rope(k), v | cache))   (mixer, after RMSNorm)
+               x = x + ffn(x)                                    (FFN, after RMSNorm)
+    logits = RMSNorm(x) @ embed.weight^T                         (tied head)
+
+and the same attention call sites: prefill attends over the unquantized K/V of
+the prompt and then appends them to the cache; decode appends the new token's K/V
+(quantized write) and runs paged decode attention over the cache
+(`attention.py:86-116`). RoPE is the interleaved-pair rotation of `model/rope.py:46-55`.
+
+The reference's only FFN is a top-k MoE (`model/moe/moe.py`); config 5 asks for a
+dense SwiGLU, which is that MoE with one expert and top-1 routing (routing weight
+1.0). It is written here as `down(silu(gate(x)) * up(x))`.
+
+What runs where: the norms (`rmsnorm_kernel`, residual add fused into the next
+norm), the cache write and the decode attention are this library's HIP kernels;
+the projections and the FFN are plain GEMMs (hipBLASLt through torch); prompt
+(prefill) attention runs in float32 PyTorch, chunked, with contiguous operands.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import torch as t
+from torch import nn
+from torch.nn import functional as F
+
+from aiproj_amd.kernals.decode_attention import decode_attention_wrapper
+from aiproj_amd.model.rmsnorm import add_rmsnorm, rmsnorm_forward
+
+
+@dataclass(frozen=True)
+class ModelConfig:
+    vocab_size: int = 32000
+    d_model: int = 2048
+    num_layers: int = 16
+    num_q_heads: int = 16
+    num_kv_heads: int = 4
+    head_dim: int = 128
+    d_ff: int = 5632
+    rope_theta: float = 10000.0
+    rms_eps: float = 1e-5
+    max_seq_len: int = 2048
+    init_std: float = 0.02
+
+
+@dataclass
+class StepMeta:
+    """What one forward needs besides the tokens (the reference's BatchMeta)."""
+
+    mode: str                          # "prefill" or "decode"
+    token_positions: t.Tensor          # [T] int64, position of every packed token
+    cache_context: object              # CacheContainer: slots, physical_blocks, block_offsets, ...
+    seq_lens: list[int] = field(default_factory=list)   # prefill only: host lengths of the packed prompts
+
+
+class RoPE(nn.Module):
+    """Interleaved-pair rotary embedding, reference `model/rope.py:4-55`."""
+
+    def __init__(self, head_dim: int, max_seq_len: int, theta: float):
+        super().__init__()
+        pairs = t.arange(head_dim // 2)
+        inv = theta ** (2 * pairs / head_dim)
+        angles = t.arange(max_seq_len)[:, None] / inv[None, :]
+        self.register_buffer("cos_table", t.cos(angles), persistent=False)
+        self.register_buffer("sin_table", t.sin(angles), persistent=False)
+
+    def forward(self, x: t.Tensor, positions: t.Tensor) -> t.Tensor:
+        cos = self.cos_table[positions].unsqueeze(-2).to(x.dtype)
+        sin = self.sin_table[positions].unsqueeze(-2).to(x.dtype)
+        first, second = x[..., 0::2], x[..., 1::2]
+        return t.stack([cos * first - sin * second, sin * first + cos * second], dim=-1).flatten(-2)
+
+
+def prefill_attention(q: t.Tensor, k: t.Tensor, v: t.Tensor, seq_lens: list[int],
+                      chunk_bytes: int = 1 << 30) -> t.Tensor:
+    """Causal GQA attention of packed prompts q [T, Hq, D], k/v [T, Hkv, D] -> [T, Hq, D].
+
+    Float32 math with contiguous operands, sequences of equal length batched
+    together in chunks whose score tensor stays under `chunk_bytes`."""
+    total, hq, d = q.shape
+    hkv = k.shape[1]
+    g = hq // hkv
+    out = t.empty_like(q)
+    start = 0
+    i = 0
+    while i < len(seq_lens):
+        length = seq_lens[i]
+        per_seq = hq * length * length * 4
+        n = 1
+        while (i + n < len(seq_lens) and seq_lens[i + n] == length and (n + 1) * per_seq <= chunk_bytes):
+            n += 1
+        end = start + n * length
+        qs = q[start:end].float().view(n, length, hkv, g, d).permute(0, 2, 3, 1, 4).contiguous()
+        ks = k[start:end].float().view(n, length, hkv, d).permute(0, 2, 3, 1).unsqueeze(2).contiguous()
+        vs = v[start:end].float().view(n, length, hkv, d).permute(0, 2, 1, 3).unsqueeze(2).contiguous()
+        scores = t.matmul(qs, ks) * (1.0 / math.sqrt(d))                      # [n, hkv, g, L, L]
+        causal = t.ones(length, length, dtype=t.bool, device=q.device).triu(1)
+        scores.masked_fill_(causal, float("-inf"))
+        probs = scores.softmax(dim=-1)
+        o = t.matmul(probs, vs)                                                # [n, hkv, g, L, d]
+        out[start:end] = o.permute(0, 3, 1, 2, 4).reshape(n * length, hq, d).to(q.dtype)
+        start = end
+        i += n
+    return out
+
+
+class Attention(nn.Module):
+    def __init__(self, cfg: ModelConfig):
+        super().__init__()
+        self.cfg = cfg
+        self.q_dim = cfg.num_q_heads * cfg.head_dim
+        self.kv_dim = cfg.num_kv_heads * cfg.head_dim
+        # q, k and v projections as one GEMM (the reference's three Linear layers, concatenated).
+        self.qkv_proj = nn.Linear(cfg.d_model, self.q_dim + 2 * self.kv_dim, bias=False)
+        self.o_proj = nn.Linear(self.q_dim, cfg.d_model, bias=False)
+        self.rope = RoPE(cfg.head_dim, cfg.max_seq_len, cfg.rope_theta)
+
+    def forward(self, h: t.Tensor, meta: StepMeta, cache) -> t.Tensor:
+        cfg = self.cfg
+        qkv = self.qkv_proj(h)
+        q = qkv[:, :self.q_dim].view(-1, cfg.num_q_heads, cfg.head_dim)
+        k = qkv[:, self.q_dim:self.q_dim + self.kv_dim].view(-1, cfg.num_kv_heads, cfg.head_dim)
+        v = qkv[:, self.q_dim + self.kv_dim:].view(-1, cfg.num_kv_heads, cfg.head_dim)
+        q = self.rope(q, meta.token_positions)
+        k = self.rope(k, meta.token_positions)
+        ctx = meta.cache_context
+        if meta.mode == "prefill":
+            out = prefill_attention(q, k, v, meta.seq_lens)
+            cache.append_kv(ctx.physical_blocks, ctx.block_offsets, k, v)
+        else:
+            cache.append_kv(ctx.physical_blocks, ctx.block_offsets, k, v)
+            out = decode_attention_wrapper(q, cache, ctx)
+        return self.o_proj(out.reshape(-1, self.q_dim))
+
+
+class SwiGLU(nn.Module):
+    def __init__(self, cfg: ModelConfig):
+        super().__init__()
+        self.d_ff = cfg.d_ff
+        self.gate_up = nn.Linear(cfg.d_model, 2 * cfg.d_ff, bias=False)
+        self.down = nn.Linear(cfg.d_ff, cfg.d_model, bias=False)
+
+    def forward(self, h: t.Tensor) -> t.Tensor:
+        gu = self.gate_up(h)
+        return self.down(F.silu(gu[:, :self.d_ff]) * gu[:, self.d_ff:])
+
+
+class DecoderLayer(nn.Module):
+    def __init__(self, cfg: ModelConfig):
+        super().__init__()
+        self.mixer_norm = nn.Parameter(t.ones(cfg.d_model))
+        self.attn = Attention(cfg)
+        self.ffn_norm = nn.Parameter(t.ones(cfg.d_model))
+        self.ffn = SwiGLU(cfg)
+
+
+class TransformerLM(nn.Module):
+    def __init__(self, cfg: ModelConfig):
+        super().__init__()
+        self.cfg = cfg
+        self.embed = nn.Embedding(cfg.vocab_size, cfg.d_model)
+        self.layers = nn.ModuleList(DecoderLayer(cfg) for _ in range(cfg.num_layers))
+        self.final_norm = nn.Parameter(t.ones(cfg.d_model))
+
+    @t.no_grad()
+    def init_weights(self, generator: t.Generator | None = None):
+        """Every matrix ~ N(0, init_std); norm weights 1."""
+        for p in self.parameters():
+            if p.ndim == 2:
+                p.normal_(0.0, self.cfg.init_std, generator=generator)
+            else:
+                p.fill_(1.0)
+        return self
+
+    @t.no_grad()
+    def forward(self, tokens: t.Tensor, meta: StepMeta, caches) -> t.Tensor:
+        """Logits [B, vocab]: of every token in decode mode (one per sequence), of each
+        prompt's last token in prefill mode."""
+        eps = self.cfg.rms_eps
+        x = self.embed(tokens)
+        h, _ = rmsnorm_forward(x, self.layers[0].mixer_norm, eps)
+        for i, layer in enumerate(self.layers):
+            a = layer.attn(h, meta, caches[i])
+            x, h = add_rmsnorm(x, a, layer.ffn_norm, eps)
+            f = layer.ffn(h)
+            nxt = self.layers[i + 1].mixer_norm if i + 1 < len(self.layers) else self.final_norm
+            x, h = add_rmsnorm(x, f, nxt, eps)
+        if meta.mode == "prefill":
+            # Only the last prompt token of each sequence is sampled from.
+            last = t.tensor(meta.seq_lens, device=h.device).cumsum(0) - 1
+            h = h[last]
+        return F.linear(h, self.embed.weight)

@@ -47,6 +47,7 @@ def parse_args():
     p.add_argument("--secondary", default="cfg2", help="second workload to report ('' for none)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-prefill", action="store_true", help="skip the prefill-size append leg")
+    p.add_argument("--no-model", action="store_true", help="skip the cfg5 model decode leg")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     return p.parse_args()
 
@@ -191,6 +192,55 @@ def prefill_write(steps: int):
         "frac": round(gbs / PEAK_HBM_GBS, 4),
         "tokens_per_s": round(tokens / (us * 1e-6)),
     }
+
+
+def model_decode(steps: int):
+    """Config 5: random-init decoder LM (16 layers, d 2048, 16q/4kv, D 128, SwiGLU
+    5632, vocab 32000, bf16 weights ~ N(0, 0.02)); 64 random-id prompts of 1024
+    tokens prefilled into the FP8 paged cache, then 128 greedy decode steps, the
+    step captured once in a HIP graph. Reports the replayed decode step."""
+    import torch as t
+    from aiproj_amd.inference.greedy_decoder import GreedyDecoder
+    from aiproj_amd.model.transformer import ModelConfig, TransformerLM
+
+    cfg = ModelConfig()
+    gen = t.Generator(device="cuda").manual_seed(6)
+    model = TransformerLM(cfg).to(device="cuda", dtype=t.bfloat16).init_weights(gen).eval()
+    batch, prompt, new = 64, 1024, 128
+    prompts = t.randint(0, cfg.vocab_size, (batch, prompt), device="cuda", generator=gen)
+    dec = GreedyDecoder(model, batch=batch, max_len=prompt + new)
+    with t.inference_mode():
+        t.cuda.synchronize()
+        t0 = time.perf_counter()
+        dec.prefill(prompts)
+        t.cuda.synchronize()
+        prefill_s = time.perf_counter() - t0
+        dec.generate(2, use_graph=True)          # eager warm-up step, capture, one replay
+        t.cuda.synchronize()
+        start, end = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+        timed = min(steps, new - 2)
+        start.record()
+        dec.generate(timed, use_graph=True)
+        end.record()
+        t.cuda.synchronize()
+    ms = start.elapsed_time(end) / timed
+    kv_bytes = cfg.num_layers * batch * (prompt + 64) * cfg.num_kv_heads * (2 * cfg.head_dim + 8)
+    weight_bytes = sum(p.numel() * p.element_size() for p in model.parameters())
+    log(f"[cfg5] decode step {ms * 1e3:.1f} us ({batch / (ms * 1e-3):.0f} tokens/s), prefill {prefill_s * 1e3:.0f} ms")
+    out = {
+        "workload": ("cfg5: 16-layer decoder LM, d 2048, 16q/4kv, D 128, SwiGLU 5632, vocab 32000, bf16 random "
+                     "weights; 64 x 1024-token prompts in the FP8 paged cache; greedy decode, step replayed "
+                     "from one HIP graph"),
+        "decode_step_ms": round(ms, 4),
+        "decode_tokens_per_s": round(batch / (ms * 1e-3), 1),
+        "timed_steps": timed,
+        "prefill_s": round(prefill_s, 3),
+        "bytes_per_step": {"weights": weight_bytes, "kv_cache_mean": kv_bytes},
+        "step_gbs": round((weight_bytes + kv_bytes) / (ms * 1e-3) / 1e9, 1),
+    }
+    del dec, model
+    t.cuda.empty_cache()
+    return out
 
 
 def copy_bandwidth_gbs(nbytes: int = 2 * 2 ** 30) -> float:
@@ -349,6 +399,7 @@ def main():
     s = main_result["setup"].spec
     cpu = None if args.no_cpu else cpu_baseline(main_result["setup"], args.cpu_seconds)
     prefill = None if args.no_prefill else prefill_write(max(10, args.steps // 2))
+    model = None if args.no_model else model_decode(100)
     kernel_gbs = main_result["kernel_gbs"]
     line = {
         "metric": METRIC,
@@ -390,6 +441,7 @@ def main():
         "cpu_baseline": cpu,
         "secondary": secondary,
         "prefill_write": prefill,
+        "model_decode": model,
     }
     print(json.dumps(line), flush=True)
 

@@ -1,0 +1,95 @@
+"""The FP8 paged KV-cache path inside a decoder LM (GPU).
+
+Follows reference tests/test_kv_cache_quantization.py:611-685: a control run keeps
+a BF16 cache holding dequantize(quantize(k)) - the numbers the FP8 cache stands for
+- and the FP8 run, forced to the control's tokens, must track its logits step by
+step (median cosine >= 0.9999, min >= 0.99). Also: a decode step captured in a HIP
+graph and replayed gives the eager tokens and logits.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch as t
+
+from aiproj_amd.inference.greedy_decoder import GreedyDecoder
+from aiproj_amd.model.transformer import ModelConfig, TransformerLM
+from tests.helpers import FP8, FP8_MAX
+
+pytestmark = pytest.mark.gpu
+
+SMALL = ModelConfig(vocab_size=256, d_model=256, num_layers=2, num_q_heads=8, num_kv_heads=2, head_dim=64,
+                    d_ff=512, max_seq_len=128)
+
+
+def small_model(seed=10, cfg=SMALL):
+    g = t.Generator(device="cuda").manual_seed(seed)
+    return TransformerLM(cfg).to(device="cuda", dtype=t.bfloat16).init_weights(g).eval()
+
+
+def fake_quantize(x):
+    x32 = x.float()
+    amax = x32.abs().amax(dim=-1, keepdim=True)
+    scale = t.where(amax > 0, amax / FP8_MAX, t.ones_like(amax))
+    codes = (x32 / scale).clamp(-FP8_MAX, FP8_MAX).to(FP8)
+    return codes.float() * scale
+
+
+def fake_quantized_caches(decoder):
+    for cache in decoder.caches:
+        store = cache.append_kv
+
+        def append_kv(blocks, offsets, ks, vs, store=store):
+            store(blocks, offsets, fake_quantize(ks), fake_quantize(vs))
+
+        cache.append_kv = append_kv
+
+
+@t.inference_mode()
+def test_fp8_decode_tracks_fake_quantized_bf16_control():
+    model = small_model()
+    prompts = t.randint(0, SMALL.vocab_size, (3, 37), device="cuda", generator=t.Generator(device="cuda").manual_seed(1))
+    steps = 40                                   # contexts reach 77 tokens: several tiles and pages
+
+    control = GreedyDecoder(model, batch=3, max_len=96, cache_dtype=t.bfloat16)
+    fake_quantized_caches(control)
+    control_first = control.prefill(prompts)
+    control_logits, forced = [], []
+    for _ in range(steps):
+        control_logits.append(control.step().float().clone())
+        forced.append(control.tokens.clone())
+
+    fp8 = GreedyDecoder(model, batch=3, max_len=96, cache_dtype=FP8)
+    fp8_first = fp8.prefill(prompts)
+    assert t.equal(fp8_first, control_first)     # prefill never reads the cache
+    sims = []
+    for i in range(steps):
+        logits = fp8.step().float()
+        fp8.tokens.copy_(forced[i])              # follow the control's tokens
+        sims.append(t.nn.functional.cosine_similarity(logits.flatten(), control_logits[i].flatten(), dim=0).item())
+    sims = t.tensor(sims)
+    assert t.isfinite(sims).all()
+    summary = f"median {sims.median():.6f}, min {sims.min():.6f}"
+    assert sims.median() >= 0.9999, summary
+    assert sims.min() >= 0.99, summary
+
+
+@t.inference_mode()
+def test_graph_replayed_decode_equals_eager_decode():
+    model = small_model(seed=11)
+    prompts = t.randint(0, SMALL.vocab_size, (4, 20), device="cuda", generator=t.Generator(device="cuda").manual_seed(2))
+    eager = GreedyDecoder(model, batch=4, max_len=64)
+    graphed = GreedyDecoder(model, batch=4, max_len=64)
+    for cache in eager.caches + graphed.caches:      # storage starts uninitialized
+        for x in (cache.k, cache.v, cache.k_scales, cache.v_scales):
+            x.view(t.uint8).zero_()
+    eager.prefill(prompts)
+    want = eager.generate(30, use_graph=False).clone()
+    graphed.prefill(prompts)
+    got = graphed.generate(30, use_graph=True).clone()
+    assert graphed.graph is not None
+    assert t.equal(got, want)
+    # The caches hold the same bytes after both runs.
+    for a, b in zip(eager.caches, graphed.caches):
+        for x, y in ((a.k, b.k), (a.v, b.v), (a.k_scales, b.k_scales), (a.v_scales, b.v_scales)):
+            assert t.equal(x.view(t.uint8), y.view(t.uint8))
