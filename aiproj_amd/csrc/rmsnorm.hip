@@ -104,18 +104,23 @@ rmsnorm_kernel(NormArgs a, int vec_ok) {
     for (int64_t r = wave0; r < a.rows; r += waves) {
         float ss = 0.0f;
         if (cached) {
-            float v[kNormChunks][kNormVec];
+            // Every load of the row (x, update, weight) is issued before the first
+            // store, so no store can order the loads behind it (outputs may alias).
+            float v[kNormChunks][kNormVec], w[kNormChunks][kNormVec];
 #pragma unroll
             for (int c = 0; c < kNormChunks; ++c) {
                 const int d0 = c * chunk + lane * kNormVec;
                 const int n = c < nchunks ? max(0, min(kNormVec, D - d0)) : 0;
                 if (n > 0) {
                     row_chunk<DT, kFused>(a, r, d0, n, vec, v[c]);
-                    if constexpr (kFused) store8<DT>(reinterpret_cast<T*>(a.state_out) + r * a.state_stride + d0, vec, n, v[c]);
+                    load8<WT>(reinterpret_cast<const W*>(a.weight) + d0, vec, n, w[c]);
                 } else {
 #pragma unroll
-                    for (int i = 0; i < kNormVec; ++i) v[c][i] = 0.0f;
+                    for (int i = 0; i < kNormVec; ++i) v[c][i] = w[c][i] = 0.0f;
                 }
+            }
+#pragma unroll
+            for (int c = 0; c < kNormChunks; ++c) {
 #pragma unroll
                 for (int i = 0; i < kNormVec; ++i) ss += v[c][i] * v[c][i];
             }
@@ -128,11 +133,11 @@ rmsnorm_kernel(NormArgs a, int vec_ok) {
                 const int d0 = c * chunk + lane * kNormVec;
                 const int n = c < nchunks ? max(0, min(kNormVec, D - d0)) : 0;
                 if (n <= 0) continue;
-                float w[kNormVec];
-                load8<WT>(reinterpret_cast<const W*>(a.weight) + d0, vec, n, w);
+                if constexpr (kFused) store8<DT>(reinterpret_cast<T*>(a.state_out) + r * a.state_stride + d0, vec, n, v[c]);
+                float o[kNormVec];
 #pragma unroll
-                for (int i = 0; i < kNormVec; ++i) v[c][i] = (v[c][i] * inv) * w[i];
-                store8<DT>(reinterpret_cast<T*>(a.out) + r * a.out_stride + d0, vec, n, v[c]);
+                for (int i = 0; i < kNormVec; ++i) o[i] = (v[c][i] * inv) * w[c][i];
+                store8<DT>(reinterpret_cast<T*>(a.out) + r * a.out_stride + d0, vec, n, o);
             }
         } else {
             for (int c = 0; c < nchunks; ++c) {

@@ -43,7 +43,8 @@ def parse_args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
-    p.add_argument("--workload", default="north", choices=["north", "cfg2", "cfg3", "cfg4", "cfg1"])
+    p.add_argument("--workload", default="north", choices=["north", "cfg2", "cfg3", "cfg4", "cfg1", "cfg5"],
+                   help="cfg5 runs only the decoder-LM leg and prints its own JSON line")
     p.add_argument("--secondary", default="cfg2", help="second workload to report ('' for none)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-prefill", action="store_true", help="skip the prefill-size append leg")
@@ -374,6 +375,10 @@ def main():
 
     _native.lib()
     log(f"device {t.cuda.get_device_name()} torch {t.__version__} lib {_native.lib().kvfp8_version().decode()}")
+
+    if args.workload == "cfg5":
+        print(json.dumps({"workload": "cfg5", "model_decode": model_decode(args.steps)}), flush=True)
+        return
 
     copy_gbs = copy_bandwidth_gbs()
     log(f"device copy bandwidth: {copy_gbs:.0f} GB/s")

@@ -150,6 +150,21 @@ int kvfp8_add_rmsnorm_forward(const void* x_dev, const void* update_dev, int dty
                               void* out_dev, int64_t out_stride, float* inv_rms_dev, void* stream);
 
 /*
+ * Interleaved-pair rotary embedding in place on heads [0, heads) of every row of x
+ * (element strides row_stride, head_stride; pairs (2i, 2i+1) of head_dim):
+ *   x0' = c x0 - s x1, x1' = s x0 + c x1,  c/s = cos/sin_table[positions[r], i]
+ * with each operation rounded to x's dtype (f32/f16/bf16) and the table values
+ * ([table_rows, head_dim / 2], table_dtype f32/f16/bf16) cast to it first. Rows
+ * whose position is outside the tables are left unchanged. positions: [rows]
+ * int32/int64.
+ * Replaces the RoPE op sequence of reference src/torch_llm/model/rope.py:46-55.
+ */
+int kvfp8_rope_inplace(void* x_dev, int dtype, int64_t rows, int32_t heads, int32_t head_dim,
+                       int64_t row_stride, int64_t head_stride, const void* positions_dev, int pos_dtype,
+                       const void* cos_table_dev, const void* sin_table_dev, int table_dtype,
+                       int64_t table_rows, void* stream);
+
+/*
  * Kernel timing hook for benchmarks (not part of the reference interface).
  * kvfp8_timing_enable(n) arms start/stop HIP events on the dispatch packets of
  * the next n decode-kernel launches (hipExtLaunchKernel, on the stream each launch

@@ -93,3 +93,22 @@ def test_graph_replayed_decode_equals_eager_decode():
     for a, b in zip(eager.caches, graphed.caches):
         for x, y in ((a.k, b.k), (a.v, b.v), (a.k_scales, b.k_scales), (a.v_scales, b.v_scales)):
             assert t.equal(x.view(t.uint8), y.view(t.uint8))
+
+
+@t.inference_mode()
+@pytest.mark.parametrize("dtype", [t.float32, t.float16, t.bfloat16])
+@pytest.mark.parametrize("table_dtype", [t.float32, "same"])
+def test_rope_kernel_is_bit_identical_to_the_reference_op_sequence(dtype, table_dtype):
+    from aiproj_amd.model.transformer import RoPE
+    rope = RoPE(64, 256, 10000.0).cuda()
+    if table_dtype == "same":
+        rope = rope.to(dtype)                   # model.to(dtype) converts the tables too
+    g = t.Generator(device="cuda").manual_seed(3)
+    x = (t.randn(50, 7 * 64, device="cuda", generator=g) * 4).to(dtype)   # 5 q/k heads + 2 untouched
+    pos = t.randint(0, 256, (50,), device="cuda", generator=g)
+    pos[7] = 300                                # outside the tables: row left unchanged
+    want = x.clone().view(50, 7, 64)
+    ok = pos < 256
+    want[ok, :5] = rope(want[ok, :5], pos[ok])
+    got = rope.apply_(x.clone(), pos, heads=5).view(50, 7, 64)
+    assert t.equal(got, want)
