@@ -5,8 +5,8 @@
 
 namespace kvfp8 {
 
-// Shapes the MFMA kernel handles (e4m3fn cache, D in {64, 128}, page size a
-// multiple of 16, group size <= 16); everything else goes to the generic kernel.
+// Shapes the MFMA kernel handles (e4m3fn or bf16 cache, D in {64, 128}, page size
+// a multiple of 16, group size <= 16); everything else goes to the generic kernel.
 bool mfma_decode_supported(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                            int64_t bt_width, int32_t block_size, int kv_dtype);
 
@@ -16,6 +16,6 @@ int64_t mfma_workspace_layout(int32_t batch, int32_t num_q_heads, int32_t num_kv
                               int64_t offsets[4]);
 
 template <int QT>
-hipError_t launch_mfma_decode(const DecodeArgs& a, void* workspace, hipStream_t stream);
+hipError_t launch_mfma_decode(const DecodeArgs& a, int kv_dtype, void* workspace, hipStream_t stream);
 
 }  // namespace kvfp8

@@ -149,50 +149,61 @@ __device__ __forceinline__ TileRef tile_ref(const MfmaArgs& a, const int32_t* ta
     return r;
 }
 
-// Loads of one 32-token step of one KV head.
-template <int C>
+// Loads of one 32-token step of one KV head. ES is the byte size of a cache
+// element: 1 for e4m3fn codes, 2 for bf16 values.
+template <int C, int ES>
 struct StepData {
-    u32x4_t ka[C];        // tile A: token (l % 16), bytes 64 c + 16 (l / 16) .. + 16
-    u32x4_t kb[C];        // tile B, same bytes
-    uint32_t v[8][C];     // rows i: token 4 (l/16) + (i % 4) of tile (i < 4 ? A : B), bytes 4C (l % 16) ..
-    float sc;             // lane l: [k|v][tile A|B][token l % 16] scale
+    u32x4_t ka[C * ES];      // tile A: token (l % 16), 16-byte runs at bytes 64 r + 16 (l / 16)
+    u32x4_t kb[C * ES];      // tile B, same runs
+    uint32_t v[8][C * ES];   // rows i: token 4 (l/16) + (i % 4) of tile (i < 4 ? A : B), 4C elements at element 4C (l % 16)
+    float sc;                // e4m3fn: lane l holds the [k|v][tile A|B][token l % 16] scale
 };
 
-template <int C>
-__device__ __forceinline__ void load_step(StepData<C>& s, const MfmaArgs& a, int h, const TileRef& ta,
+template <int C, int ES>
+__device__ __forceinline__ void load_step(StepData<C, ES>& s, const MfmaArgs& a, int h, const TileRef& ta,
                                           const TileRef& tb, int lane) {
     constexpr int D = 64 * C;
     constexpr int NB = 4 * C;
+    constexpr int KR = C * ES;
+    constexpr int VW = C * ES;
     const int m16 = lane & 15, j = lane >> 4;
     const int32_t hkv = a.d.num_kv_heads;
-    const int32_t row_stride = hkv * D;
-    const int64_t ea = (ta.row0 * hkv + h) * D;
-    const int64_t eb = (tb.row0 * hkv + h) * D;
+    const int32_t row_stride = hkv * D * ES;                 // bytes between tokens
+    const int64_t ea = (ta.row0 * hkv + h) * D * ES;
+    const int64_t eb = (tb.row0 * hkv + h) * D * ES;
     const uint8_t* kc = reinterpret_cast<const uint8_t*>(a.d.k_cache);
     const uint8_t* vc = reinterpret_cast<const uint8_t*>(a.d.v_cache);
     const uint32_t koff = (uint32_t)(m16 * row_stride + 16 * j);
-    // K rows are read as two 64-byte halves by two instructions (normal loads
+    // K rows are read as 64-byte pieces by separate instructions (normal loads
     // keep the line in L2 between them); every V instruction reads whole
-    // 128-byte rows, streamed with nontemporal loads.
+    // rows, streamed with nontemporal loads.
 #pragma unroll
-    for (int c = 0; c < C; ++c) {
-        s.ka[c] = *reinterpret_cast<const u32x4_t*>(kc + ea + koff + 64 * c);
-        s.kb[c] = *reinterpret_cast<const u32x4_t*>(kc + eb + koff + 64 * c);
+    for (int r = 0; r < KR; ++r) {
+        s.ka[r] = *reinterpret_cast<const u32x4_t*>(kc + ea + koff + 64 * r);
+        s.kb[r] = *reinterpret_cast<const u32x4_t*>(kc + eb + koff + 64 * r);
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const uint8_t* p = vc + (i < 4 ? ea : eb) + (uint32_t)((4 * j + (i & 3)) * row_stride + NB * m16);
-        if constexpr (C == 1) {
+        const uint8_t* p = vc + (i < 4 ? ea : eb) + (uint32_t)((4 * j + (i & 3)) * row_stride + NB * ES * m16);
+        if constexpr (VW == 1) {
             s.v[i][0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
-        } else {
+        } else if constexpr (VW == 2) {
             const u32x2_t x = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p));
             s.v[i][0] = x.x;
             s.v[i][1] = x.y;
+        } else {
+            const u32x4_t x = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+            s.v[i][0] = x.x;
+            s.v[i][1] = x.y;
+            s.v[i][2] = x.z;
+            s.v[i][3] = x.w;
         }
     }
-    const int kv = lane >> 5, which = (lane >> 4) & 1;
-    const int64_t r = (which ? tb.row0 : ta.row0) + m16;
-    s.sc = (kv ? a.d.v_scales : a.d.k_scales)[r * hkv + h];
+    if constexpr (ES == 1) {
+        const int kv = lane >> 5, which = (lane >> 4) & 1;
+        const int64_t r = (which ? tb.row0 : ta.row0) + m16;
+        s.sc = (kv ? a.d.v_scales : a.d.k_scales)[r * hkv + h];
+    }
 }
 
 // Online-softmax state of one wave (one KV head, its G q heads in columns g).
@@ -203,35 +214,57 @@ struct WaveState {
     float l;              // this lane's share of the softmax denominator
 };
 
-template <int C, bool kHiLo>
-__device__ __forceinline__ void compute_step(WaveState<C>& st, const StepData<C>& s, const bf16x8_t* qh,
+// Dimension of Q feeding element i of the QK MFMA kb in lane group j: the same
+// permutation of the head dimension as the K runs of load_step.
+template <int ES>
+__device__ __forceinline__ int qk_dim(int kb, int j, int i) {
+    if constexpr (ES == 1) return 64 * (kb >> 1) + 16 * j + 8 * (kb & 1) + i;   // 16 codes per run, 2 MFMAs
+    else return 32 * kb + 8 * j + i;                                             // 8 values per run, 1 MFMA
+}
+
+template <int C, int ES, bool kHiLo>
+__device__ __forceinline__ void compute_step(WaveState<C>& st, const StepData<C, ES>& s, const bf16x8_t* qh,
                                              const bf16x8_t* ql, float4* stage, int lane, int lim_a,
                                              int lim_b, float score_scale) {
+    constexpr int VW = C * ES;
     const int j = lane >> 4;
     const bool full = lim_a == 16 && lim_b == 16;   // wave-uniform
 
-    // Scales through this wave's LDS slot: [k|v][tile][token] -> 4 consecutive
-    // tokens per read. The k scale carries sm_scale * log2(e).
-    float* stage_f = reinterpret_cast<float*>(stage);
-    stage_f[lane] = lane < 32 ? s.sc * score_scale : s.sc;
-    __builtin_amdgcn_wave_barrier();
-    const float4 ks_a = stage[j], ks_b = stage[4 + j], vs_a = stage[8 + j], vs_b = stage[12 + j];
-    __builtin_amdgcn_wave_barrier();
+    float4 ks_a, ks_b, vs_a, vs_b;
+    if constexpr (ES == 1) {
+        // Scales through this wave's LDS slot: [k|v][tile][token] -> 4 consecutive
+        // tokens per read. The k scale carries sm_scale * log2(e).
+        float* stage_f = reinterpret_cast<float*>(stage);
+        stage_f[lane] = lane < 32 ? s.sc * score_scale : s.sc;
+        __builtin_amdgcn_wave_barrier();
+        ks_a = stage[j];
+        ks_b = stage[4 + j];
+        vs_a = stage[8 + j];
+        vs_b = stage[12 + j];
+        __builtin_amdgcn_wave_barrier();
+    } else {
+        ks_a = ks_b = make_float4(score_scale, score_scale, score_scale, score_scale);
+        vs_a = vs_b = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+    }
 
     // Scores of the two tiles.
     f32x4_t sa = {0.0f, 0.0f, 0.0f, 0.0f}, sb = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int c = 0; c < C; ++c) {
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            const bf16x8_t ka = fp8x8(s.ka[c][2 * half], s.ka[c][2 * half + 1]);
-            const bf16x8_t kb = fp8x8(s.kb[c][2 * half], s.kb[c][2 * half + 1]);
-            sa = mma(ka, qh[2 * c + half], sa);
-            sb = mma(kb, qh[2 * c + half], sb);
-            if constexpr (kHiLo) {
-                sa = mma(ka, ql[2 * c + half], sa);
-                sb = mma(kb, ql[2 * c + half], sb);
-            }
+    for (int kb = 0; kb < 2 * C; ++kb) {
+        bf16x8_t ka, kbv;
+        if constexpr (ES == 1) {
+            const int c = kb >> 1, half = kb & 1;
+            ka = fp8x8(s.ka[c][2 * half], s.ka[c][2 * half + 1]);
+            kbv = fp8x8(s.kb[c][2 * half], s.kb[c][2 * half + 1]);
+        } else {
+            ka = __builtin_bit_cast(bf16x8_t, s.ka[kb]);
+            kbv = __builtin_bit_cast(bf16x8_t, s.kb[kb]);
+        }
+        sa = mma(ka, qh[kb], sa);
+        sb = mma(kbv, qh[kb], sb);
+        if constexpr (kHiLo) {
+            sa = mma(ka, ql[kb], sa);
+            sb = mma(kbv, ql[kb], sb);
         }
     }
     float sc[8] = {sa[0] * ks_a.x, sa[1] * ks_a.y, sa[2] * ks_a.z, sa[3] * ks_a.w,
@@ -281,36 +314,51 @@ __device__ __forceinline__ void compute_step(WaveState<C>& st, const StepData<C>
         if constexpr (kHiLo) pl[i] = (__bf16)(pv[i] - (float)ph[i]);
     }
 
-    // V rows: zero the rows of masked tokens (stale pages may hold NaN codes).
-    uint32_t vr[8][C];
+    // V rows: zero the rows of masked tokens (stale pages may hold NaN).
+    uint32_t vr[8][VW];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const bool live = full || (4 * j + (i & 3) < (i < 4 ? lim_a : lim_b));
 #pragma unroll
-        for (int c = 0; c < C; ++c) vr[i][c] = live ? s.v[i][c] : 0u;
+        for (int c = 0; c < VW; ++c) vr[i][c] = live ? s.v[i][c] : 0u;
     }
+    if constexpr (ES == 1) {
+        // Byte transpose: pair the codes of rows (2p, 2p + 1) at one column, widen.
 #pragma unroll
-    for (int c = 0; c < C; ++c) {
-        bf16x2_t e[4][4];
+        for (int c = 0; c < C; ++c) {
+            bf16x2_t e[4][4];
 #pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            const uint32_t x = __builtin_amdgcn_perm(vr[2 * p + 1][c], vr[2 * p][c], 0x05010400u);
-            const uint32_t y = __builtin_amdgcn_perm(vr[2 * p + 1][c], vr[2 * p][c], 0x07030602u);
-            e[0][p] = fp8x2_lo(x);
-            e[1][p] = fp8x2_hi(x);
-            e[2][p] = fp8x2_lo(y);
-            e[3][p] = fp8x2_hi(y);
+            for (int p = 0; p < 4; ++p) {
+                const uint32_t x = __builtin_amdgcn_perm(vr[2 * p + 1][c], vr[2 * p][c], 0x05010400u);
+                const uint32_t y = __builtin_amdgcn_perm(vr[2 * p + 1][c], vr[2 * p][c], 0x07030602u);
+                e[0][p] = fp8x2_lo(x);
+                e[1][p] = fp8x2_hi(x);
+                e[2][p] = fp8x2_lo(y);
+                e[3][p] = fp8x2_hi(y);
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const bf16x8_t av = cat8(e[q][0], e[q][1], e[q][2], e[q][3]);
+                st.o[4 * c + q] = mma(av, ph, st.o[4 * c + q]);
+                if constexpr (kHiLo) st.o[4 * c + q] = mma(av, pl, st.o[4 * c + q]);
+            }
         }
+    } else {
+        // 16-bit transpose: element nb of rows (2p, 2p + 1) into one dword.
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const bf16x8_t av = cat8(e[q][0], e[q][1], e[q][2], e[q][3]);
-            st.o[4 * c + q] = mma(av, ph, st.o[4 * c + q]);
-            if constexpr (kHiLo) st.o[4 * c + q] = mma(av, pl, st.o[4 * c + q]);
+        for (int nb = 0; nb < 4 * C; ++nb) {
+            const uint32_t sel = (nb & 1) ? 0x07060302u : 0x05040100u;
+            u32x4_t w;
+#pragma unroll
+            for (int p = 0; p < 4; ++p) w[p] = __builtin_amdgcn_perm(vr[2 * p + 1][nb >> 1], vr[2 * p][nb >> 1], sel);
+            const bf16x8_t av = __builtin_bit_cast(bf16x8_t, w);
+            st.o[nb] = mma(av, ph, st.o[nb]);
+            if constexpr (kHiLo) st.o[nb] = mma(av, pl, st.o[nb]);
         }
     }
 }
 
-template <int C, int QT>
+template <int C, int QT, int ES>
 __global__ void __launch_bounds__(kMaxThreads)
 decode_mfma_kernel(MfmaArgs a) {
     constexpr int D = 64 * C;
@@ -362,18 +410,21 @@ decode_mfma_kernel(MfmaArgs a) {
             st.m = kNegInf;
             st.l = 0.0f;
 
-            // Three-buffer pipeline: the loads of steps T + 2 and T + 4 are in
-            // flight while step T is computed.
-            StepData<C> buf0, buf1, buf2;
+            // Load pipeline: e4m3fn keeps the loads of steps T + 2 and T + 4 in
+            // flight while step T is computed (three buffers); bf16 steps are twice
+            // the bytes and keep one step in flight (two buffers).
+            StepData<C, ES> buf0, buf1, buf2;
             TileRef r0a, r0b, r1a, r1b, r2a, r2b;
-            auto issue = [&](StepData<C>& dst, int32_t tile0, TileRef& ra, TileRef& rb) {
+            auto issue = [&](StepData<C, ES>& dst, int32_t tile0, TileRef& ra, TileRef& rb) {
                 ra = tile_ref(a, table_row, tile0);
                 rb = tile0 + 1 < t1 ? tile_ref(a, table_row, tile0 + 1) : TileRef{0, 0};
-                load_step<C>(dst, a, h, ra, rb, lane);
+                load_step<C, ES>(dst, a, h, ra, rb, lane);
             };
             int32_t T = t0;
             issue(buf0, T, r0a, r0b);
-            if (T + 2 < t1) issue(buf1, T + 2, r1a, r1b);
+            if constexpr (ES == 1) {
+                if (T + 2 < t1) issue(buf1, T + 2, r1a, r1b);
+            }
 
             // Q^T operand of this head's G query heads (columns g >= G are zero),
             // loaded while the first KV steps are in flight.
@@ -381,39 +432,48 @@ decode_mfma_kernel(MfmaArgs a) {
             const int hq = h * G + m16;
             const bool qlive = m16 < G;
 #pragma unroll
-            for (int c = 0; c < C; ++c) {
+            for (int kb = 0; kb < 2 * C; ++kb) {
 #pragma unroll
-                for (int half = 0; half < 2; ++half) {
-                    const int d0 = 64 * c + 16 * j + 8 * half;
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) {
-                        const float x = qlive ? load_q<QT>(a.d, b, hq, d0 + i) : 0.0f;
-                        const __bf16 hi = (__bf16)x;
-                        qh[2 * c + half][i] = hi;
-                        if constexpr (kHiLo) ql[2 * c + half][i] = (__bf16)(x - (float)hi);
-                    }
+                for (int i = 0; i < 8; ++i) {
+                    const float x = qlive ? load_q<QT>(a.d, b, hq, qk_dim<ES>(kb, j, i)) : 0.0f;
+                    const __bf16 hi = (__bf16)x;
+                    qh[kb][i] = hi;
+                    if constexpr (kHiLo) ql[kb][i] = (__bf16)(x - (float)hi);
                 }
             }
 
-            auto compute = [&](const StepData<C>& cur, int32_t tile0, const TileRef& ra, const TileRef& rb) {
+            auto compute = [&](const StepData<C, ES>& cur, int32_t tile0, const TileRef& ra, const TileRef& rb) {
                 const int64_t pos = (int64_t)tile0 * 16;
                 const int lim_a = ra.valid ? (int)max((int64_t)0, min((int64_t)16, len - pos)) : 0;
                 const int lim_b = rb.valid ? (int)max((int64_t)0, min((int64_t)16, len - pos - 16)) : 0;
-                compute_step<C, kHiLo>(st, cur, qh, ql, stage, lane, lim_a, lim_b, a.d.score_scale);
+                compute_step<C, ES, kHiLo>(st, cur, qh, ql, stage, lane, lim_a, lim_b, a.d.score_scale);
             };
-            while (true) {
-                if (T + 4 < t1) issue(buf2, T + 4, r2a, r2b);
-                compute(buf0, T, r0a, r0b);
-                T += 2;
-                if (T >= t1) break;
-                if (T + 4 < t1) issue(buf0, T + 4, r0a, r0b);
-                compute(buf1, T, r1a, r1b);
-                T += 2;
-                if (T >= t1) break;
-                if (T + 4 < t1) issue(buf1, T + 4, r1a, r1b);
-                compute(buf2, T, r2a, r2b);
-                T += 2;
-                if (T >= t1) break;
+            if constexpr (ES == 1) {
+                while (true) {
+                    if (T + 4 < t1) issue(buf2, T + 4, r2a, r2b);
+                    compute(buf0, T, r0a, r0b);
+                    T += 2;
+                    if (T >= t1) break;
+                    if (T + 4 < t1) issue(buf0, T + 4, r0a, r0b);
+                    compute(buf1, T, r1a, r1b);
+                    T += 2;
+                    if (T >= t1) break;
+                    if (T + 4 < t1) issue(buf1, T + 4, r1a, r1b);
+                    compute(buf2, T, r2a, r2b);
+                    T += 2;
+                    if (T >= t1) break;
+                }
+            } else {
+                while (true) {
+                    if (T + 2 < t1) issue(buf1, T + 2, r1a, r1b);
+                    compute(buf0, T, r0a, r0b);
+                    T += 2;
+                    if (T >= t1) break;
+                    if (T + 2 < t1) issue(buf0, T + 2, r0a, r0b);
+                    compute(buf1, T, r1a, r1b);
+                    T += 2;
+                    if (T >= t1) break;
+                }
             }
 
             // Denominator: sum the four lane groups of each column.
@@ -560,25 +620,25 @@ int64_t max_groups(int32_t num_kv_heads) {
     return (int64_t)device_cus() * (per_cu > 0 ? per_cu : 1);
 }
 
-template <int C, int QT>
+template <int C, int QT, int ES>
 hipError_t launch_c(const MfmaArgs& a, int64_t cap, hipStream_t s) {
     const int threads = 64 * waves_for(a.d.num_kv_heads);
     const size_t lds = (size_t)(a.d.batch + 1) * sizeof(int32_t);
     // Resident workgroups per CU, queried once per (device, workgroup size); the
     // dynamic LDS (<= 32 KiB) never limits residency at these sizes.
-    static int resident[64][kMaxWaves + 1] = {};
+    static int resident[64][kMaxWaves + 1] = {};     // per template instance
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
     int& per_cu = resident[dev][threads / 64];
     if (per_cu == 0) {
-        const void* fn = reinterpret_cast<const void*>(&decode_mfma_kernel<C, QT>);
+        const void* fn = reinterpret_cast<const void*>(&decode_mfma_kernel<C, QT, ES>);
         int n = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, threads, lds) != hipSuccess || n <= 0) n = 1;
         per_cu = n;
     }
     int64_t groups = (int64_t)device_cus() * per_cu;
     groups = groups < cap ? groups : cap;
-    const hipError_t err = launch_timed(decode_mfma_kernel<C, QT>, dim3((unsigned)groups), dim3(threads), lds, s,
+    const hipError_t err = launch_timed(decode_mfma_kernel<C, QT, ES>, dim3((unsigned)groups), dim3(threads), lds, s,
                                         next_kernel_timing(), a);
     if (err != hipSuccess) return err;
     const int64_t pairs = (int64_t)a.d.batch * a.d.num_q_heads;
@@ -590,7 +650,7 @@ hipError_t launch_c(const MfmaArgs& a, int64_t cap, hipStream_t s) {
 
 bool mfma_decode_supported(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                            int64_t bt_width, int32_t block_size, int kv_dtype) {
-    if (kv_dtype != KVFP8_E4M3FN) return false;
+    if (kv_dtype != KVFP8_E4M3FN && kv_dtype != KVFP8_BF16) return false;
     if (head_dim != 64 && head_dim != 128) return false;
     if (block_size < 16 || block_size % 16 != 0) return false;
     if (num_q_heads % num_kv_heads != 0 || num_q_heads / num_kv_heads > 16) return false;
@@ -623,7 +683,7 @@ int64_t mfma_workspace_layout(int32_t batch, int32_t num_q_heads, int32_t num_kv
 }
 
 template <int QT>
-hipError_t launch_mfma_decode(const DecodeArgs& d, void* workspace, hipStream_t stream) {
+hipError_t launch_mfma_decode(const DecodeArgs& d, int kv_dtype, void* workspace, hipStream_t stream) {
     int64_t off[4];
     mfma_workspace_layout(d.batch, d.num_q_heads, d.num_kv_heads, d.head_dim, off);
     char* ws = reinterpret_cast<char*>(workspace);
@@ -635,12 +695,13 @@ hipError_t launch_mfma_decode(const DecodeArgs& d, void* workspace, hipStream_t 
     a.part_l = reinterpret_cast<float*>(ws + off[2]);
     a.part_acc = reinterpret_cast<float*>(ws + off[3]);
     const int64_t cap = max_groups(d.num_kv_heads);
-    if (d.head_dim == 64) return launch_c<1, QT>(a, cap, stream);
-    return launch_c<2, QT>(a, cap, stream);
+    if (kv_dtype == KVFP8_BF16)
+        return d.head_dim == 64 ? launch_c<1, QT, 2>(a, cap, stream) : launch_c<2, QT, 2>(a, cap, stream);
+    return d.head_dim == 64 ? launch_c<1, QT, 1>(a, cap, stream) : launch_c<2, QT, 1>(a, cap, stream);
 }
 
-template hipError_t launch_mfma_decode<KVFP8_F32>(const DecodeArgs&, void*, hipStream_t);
-template hipError_t launch_mfma_decode<KVFP8_F16>(const DecodeArgs&, void*, hipStream_t);
-template hipError_t launch_mfma_decode<KVFP8_BF16>(const DecodeArgs&, void*, hipStream_t);
+template hipError_t launch_mfma_decode<KVFP8_F32>(const DecodeArgs&, int, void*, hipStream_t);
+template hipError_t launch_mfma_decode<KVFP8_F16>(const DecodeArgs&, int, void*, hipStream_t);
+template hipError_t launch_mfma_decode<KVFP8_BF16>(const DecodeArgs&, int, void*, hipStream_t);
 
 }  // namespace kvfp8

@@ -49,6 +49,7 @@ def parse_args():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-prefill", action="store_true", help="skip the prefill-size append leg")
     p.add_argument("--no-model", action="store_true", help="skip the cfg5 model decode leg")
+    p.add_argument("--no-others", action="store_true", help="skip the cfg1/cfg3/cfg4 decode legs")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     return p.parse_args()
 
@@ -403,6 +404,24 @@ def main():
 
     s = main_result["setup"].spec
     cpu = None if args.no_cpu else cpu_baseline(main_result["setup"], args.cpu_seconds)
+    others = {}
+    if not args.no_others:
+        for name in ("cfg1", "cfg3", "cfg4"):
+            if name == args.workload:
+                continue
+            r = measure(name, max(10, args.steps // 2), max(3, args.warmup // 2))
+            spec = r["setup"].spec
+            others[name] = {
+                "batch": spec.batch, "heads": f"{spec.num_q_heads}q/{spec.num_kv_heads}kv", "head_dim": spec.head_dim,
+                "kv_tokens": spec.total_tokens,
+                "step_us": round(r["ms_per_step"] * 1e3, 2),
+                "step_gbs": round(r["gbs"], 1),
+                "decode_kernel_us": round(r["split_kernel_ms"] * 1e3, 2),
+                "decode_kernel_gbs": round(r["kernel_gbs"], 1),
+                "decode_kernel_frac": round(r["kernel_gbs"] / PEAK_HBM_GBS, 4),
+                "kv_tokens_per_s": round(r["kv_tokens_per_s"]),
+            }
+            del r
     prefill = None if args.no_prefill else prefill_write(max(10, args.steps // 2))
     model = None if args.no_model else model_decode(100)
     kernel_gbs = main_result["kernel_gbs"]
@@ -445,6 +464,7 @@ def main():
         },
         "cpu_baseline": cpu,
         "secondary": secondary,
+        "other_workloads": others,
         "prefill_write": prefill,
         "model_decode": model,
     }
