@@ -30,11 +30,18 @@
 // The reduction index of each product may be permuted freely as long as both
 // operands use the same permutation; the kernel picks the permutations that let
 // every lane load long contiguous runs:
-//   * QK: lane l reads 16-byte runs of token (l % 16) at byte 64 c + 16 (l / 16);
-//     bytes 8h..8h+7 of run c feed MFMA 2c + h.
+//   * QK, e4m3fn with D = 128 (whole-row K): an MFMA row is (token t of an
+//     8-token sub-tile, half h of D) = 2t + h and a column is (q head g, half
+//     h') = g + 8h', so lane 2t + h + 16j reads the 16 bytes at 64h + 16j of
+//     token t and one load instruction covers eight whole 128-byte rows. The
+//     score of (t, g) is the sum of the two diagonal blocks h = h', which sit 8
+//     lanes apart (one DPP row rotate). q heads 8..15 use a second set of
+//     products.
+//   * QK otherwise: lane l reads 16-byte runs of token (l % 16) at byte 64 c +
+//     16 (l / 16); bytes 8h..8h+7 of run c feed MFMA 2c + h.
 //   * PV: lane l reads 4C contiguous bytes at column 4C (l % 16) of eight token
-//     rows: tokens 4 (l/16) + i of tile A (i < 4) and of tile B (i >= 4), the
-//     same tokens its QK output column holds. v_perm_b32 pairs rows (2p, 2p+1)
+//     rows: tokens step_token(i, l / 16) of tile A (i < 4) and of tile B
+//     (i >= 4), the same tokens its scores belong to. v_perm_b32 pairs rows (2p, 2p+1)
 //     of one column and v_cvt_scalef32_pk_bf16_fp8 widens the pair.
 #include "kvfp8_decode_mfma.h"
 
@@ -97,6 +104,22 @@ __device__ __forceinline__ f32x4_t mma(bf16x8_t a, bf16x8_t b, f32x4_t c) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Value of lane (l ^ 8) (DPP row_ror:8 inside each row of 16 lanes).
+__device__ __forceinline__ float row_ror8(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x128, 0xF, 0xF, false));
+}
+
+// The e4m3fn D = 128 kernel reads K in whole 128-byte rows (see load_step).
+template <int C, int ES>
+constexpr bool kWholeRowK = ES == 1 && C == 2;
+
+// Token (within its 16-token tile, tile i / 4) of score i and V row i of lane group j.
+template <bool kWL>
+__device__ __forceinline__ int step_token(int i, int j) {
+    if constexpr (kWL) return 8 * ((i >> 1) & 1) + 2 * j + (i & 1);
+    else return 4 * j + (i & 3);
+}
+
 // Tile prefix over the batch in LDS: prefix[b] = sum_{i<b} ceil(len_i / 16).
 // Per-thread runs, a shuffle scan inside each wave, then the wave totals.
 __device__ void build_tile_prefix(const DecodeArgs& a, int32_t* prefix, int32_t* wave_total) {
@@ -154,8 +177,9 @@ __device__ __forceinline__ TileRef tile_ref(const MfmaArgs& a, const int32_t* ta
 template <int C, int ES>
 struct StepData {
     u32x4_t ka[C * ES];      // tile A: token (l % 16), 16-byte runs at bytes 64 r + 16 (l / 16)
+                             // (whole-row K: run r holds token 8r + (l % 16) / 2 at byte 64 (l % 2) + 16 (l / 16))
     u32x4_t kb[C * ES];      // tile B, same runs
-    uint32_t v[8][C * ES];   // rows i: token 4 (l/16) + (i % 4) of tile (i < 4 ? A : B), 4C elements at element 4C (l % 16)
+    uint32_t v[8][C * ES];   // rows i: token step_token(i, l / 16) of tile (i < 4 ? A : B), 4C elements at element 4C (l % 16)
     float sc;                // e4m3fn: lane l holds the [k|v][tile A|B][token l % 16] scale
 };
 
@@ -173,18 +197,37 @@ __device__ __forceinline__ void load_step(StepData<C, ES>& s, const MfmaArgs& a,
     const int64_t eb = (tb.row0 * hkv + h) * D * ES;
     const uint8_t* kc = reinterpret_cast<const uint8_t*>(a.d.k_cache);
     const uint8_t* vc = reinterpret_cast<const uint8_t*>(a.d.v_cache);
-    const uint32_t koff = (uint32_t)(m16 * row_stride + 16 * j);
-    // K rows are read as 64-byte pieces by separate instructions (normal loads
-    // keep the line in L2 between them); every V instruction reads whole
-    // rows, streamed with nontemporal loads.
+    constexpr bool kWL = kWholeRowK<C, ES>;
+    if constexpr (kWL) {
+        // Lane 2t + h + 16 j reads bytes 64 h + 16 j .. + 15 of token t (8 tokens
+        // per instruction): every instruction reads eight whole 128-byte rows,
+        // streamed with nontemporal loads.
+        const uint32_t koff = (uint32_t)((m16 >> 1) * row_stride + 64 * (m16 & 1) + 16 * j);
 #pragma unroll
-    for (int r = 0; r < KR; ++r) {
-        s.ka[r] = *reinterpret_cast<const u32x4_t*>(kc + ea + koff + 64 * r);
-        s.kb[r] = *reinterpret_cast<const u32x4_t*>(kc + eb + koff + 64 * r);
+        for (int r = 0; r < KR; ++r) {
+            s.ka[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(kc + ea + koff + 8 * r * row_stride));
+            s.kb[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(kc + eb + koff + 8 * r * row_stride));
+        }
+    } else {
+        // Token (l % 16), 16-byte runs at 64 r + 16 (l / 16). With D = 64 codes a
+        // run set is the whole row (nontemporal); wider rows are read as pieces
+        // by separate instructions, and normal loads keep the line in L2 between them.
+        const uint32_t koff = (uint32_t)(m16 * row_stride + 16 * j);
+#pragma unroll
+        for (int r = 0; r < KR; ++r) {
+            if constexpr (KR == 1) {
+                s.ka[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(kc + ea + koff + 64 * r));
+                s.kb[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(kc + eb + koff + 64 * r));
+            } else {
+                s.ka[r] = *reinterpret_cast<const u32x4_t*>(kc + ea + koff + 64 * r);
+                s.kb[r] = *reinterpret_cast<const u32x4_t*>(kc + eb + koff + 64 * r);
+            }
+        }
     }
+    // Every V instruction reads whole rows (nontemporal).
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const uint8_t* p = vc + (i < 4 ? ea : eb) + (uint32_t)((4 * j + (i & 3)) * row_stride + NB * ES * m16);
+        const uint8_t* p = vc + (i < 4 ? ea : eb) + (uint32_t)(step_token<kWL>(i, j) * row_stride + NB * ES * m16);
         if constexpr (VW == 1) {
             s.v[i][0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
         } else if constexpr (VW == 2) {
@@ -214,15 +257,24 @@ struct WaveState {
     float l;              // this lane's share of the softmax denominator
 };
 
-// Dimension of Q feeding element i of the QK MFMA kb in lane group j: the same
-// permutation of the head dimension as the K runs of load_step.
-template <int ES>
-__device__ __forceinline__ int qk_dim(int kb, int j, int i) {
-    if constexpr (ES == 1) return 64 * (kb >> 1) + 16 * j + 8 * (kb & 1) + i;   // 16 codes per run, 2 MFMAs
-    else return 32 * kb + 8 * j + i;                                             // 8 values per run, 1 MFMA
+// Q head column and dimension feeding element i of Q^T operand kb in lane
+// (c = l % 16, j = l / 16): the same permutation of the head dimension as the K
+// runs of load_step. Whole-row K: operand kb = 2 set + m holds column (g, h') =
+// c, head g = c % 8 + 8 set, dims of half h' = c / 8.
+template <int C, int ES>
+__device__ __forceinline__ int qk_head(int kb, int c) {
+    if constexpr (kWholeRowK<C, ES>) return (c & 7) + 8 * (kb >> 1);
+    else return c;
+}
+template <int C, int ES>
+__device__ __forceinline__ int qk_dim(int kb, int c, int j, int i) {
+    if constexpr (kWholeRowK<C, ES>) return 64 * (c >> 3) + 16 * j + 8 * (kb & 1) + i;
+    else if constexpr (ES == 1) return 64 * (kb >> 1) + 16 * j + 8 * (kb & 1) + i;   // 16 codes per run, 2 MFMAs
+    else return 32 * kb + 8 * j + i;                                                  // 8 values per run, 1 MFMA
 }
 
-template <int C, int ES, bool kHiLo>
+// kSets = 2: whole-row K with G > 8 (a second set of QK products for heads 8..15).
+template <int C, int ES, bool kHiLo, int kSets>
 __device__ __forceinline__ void compute_step(WaveState<C>& st, const StepData<C, ES>& s, const bf16x8_t* qh,
                                              const bf16x8_t* ql, float4* stage, int lane, int lim_a,
                                              int lim_b, float score_scale) {
@@ -230,51 +282,120 @@ __device__ __forceinline__ void compute_step(WaveState<C>& st, const StepData<C,
     const int j = lane >> 4;
     const bool full = lim_a == 16 && lim_b == 16;   // wave-uniform
 
-    float4 ks_a, ks_b, vs_a, vs_b;
+    constexpr bool kWL = kWholeRowK<C, ES>;
+    // Per-token scales of score i (k, with sm_scale * log2(e)) and V row i (v).
+    float ks[8], vs[8];
     if constexpr (ES == 1) {
-        // Scales through this wave's LDS slot: [k|v][tile][token] -> 4 consecutive
-        // tokens per read. The k scale carries sm_scale * log2(e).
+        // Through this wave's LDS slot: lane l holds the scale of [k|v] (l / 32),
+        // step token l % 32, stored so that each lane reads its 8 tokens as two
+        // float4 runs.
         float* stage_f = reinterpret_cast<float*>(stage);
-        stage_f[lane] = lane < 32 ? s.sc * score_scale : s.sc;
+        int widx = lane;
+        if constexpr (kWL) {
+            const int p = lane & 31;    // step token 8 x + 2 j' + s -> slot 8 j' + 2 x + s
+            widx = (lane & 32) + 8 * ((p >> 1) & 3) + 2 * (p >> 3) + (p & 1);
+        }
+        stage_f[widx] = lane < 32 ? s.sc * score_scale : s.sc;
         __builtin_amdgcn_wave_barrier();
-        ks_a = stage[j];
-        ks_b = stage[4 + j];
-        vs_a = stage[8 + j];
-        vs_b = stage[12 + j];
+        float4 k0, k1, v0, v1;
+        if constexpr (kWL) {
+            k0 = stage[2 * j];
+            k1 = stage[2 * j + 1];
+            v0 = stage[8 + 2 * j];
+            v1 = stage[9 + 2 * j];
+        } else {
+            k0 = stage[j];
+            k1 = stage[4 + j];
+            v0 = stage[8 + j];
+            v1 = stage[12 + j];
+        }
         __builtin_amdgcn_wave_barrier();
+        ks[0] = k0.x; ks[1] = k0.y; ks[2] = k0.z; ks[3] = k0.w;
+        ks[4] = k1.x; ks[5] = k1.y; ks[6] = k1.z; ks[7] = k1.w;
+        vs[0] = v0.x; vs[1] = v0.y; vs[2] = v0.z; vs[3] = v0.w;
+        vs[4] = v1.x; vs[5] = v1.y; vs[6] = v1.z; vs[7] = v1.w;
     } else {
-        ks_a = ks_b = make_float4(score_scale, score_scale, score_scale, score_scale);
-        vs_a = vs_b = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            ks[i] = score_scale;
+            vs[i] = 1.0f;
+        }
     }
 
-    // Scores of the two tiles.
-    f32x4_t sa = {0.0f, 0.0f, 0.0f, 0.0f}, sb = {0.0f, 0.0f, 0.0f, 0.0f};
+    // Scores of the 32 tokens, 8 per lane: score i is token step_token(i, j) of
+    // tile i / 4.
+    float sc[8];
+    if constexpr (kWL) {
+        // Sub-tile x (tokens 8x .. 8x + 7 of the step): MFMA rows are (token t,
+        // half h of D) = 2t + h, columns (q head g, half h') = g + 8h' for the q
+        // heads g < 8 (set 0) and, with G > 8, 8 + g (set 1). D[(t, h)][(g, h')]
+        // is the dot product over half h of K with half h' of Q, so the score of
+        // (t, g) is D[(t,0)][(g,0)] + D[(t,1)][(g,1)]: register 2s of lane c and
+        // register 2s + 1 of lane c + 8 (c < 8, token t = 2 j + s). Lane c keeps
+        // its half and takes its partner's through a row rotate by 8; lanes
+        // c >= 8 end with the scores of column c (set 1) or a copy of column c - 8.
+        const bool upper = (lane & 8) != 0;
 #pragma unroll
-    for (int kb = 0; kb < 2 * C; ++kb) {
-        bf16x8_t ka, kbv;
-        if constexpr (ES == 1) {
-            const int c = kb >> 1, half = kb & 1;
-            ka = fp8x8(s.ka[c][2 * half], s.ka[c][2 * half + 1]);
-            kbv = fp8x8(s.kb[c][2 * half], s.kb[c][2 * half + 1]);
-        } else {
-            ka = __builtin_bit_cast(bf16x8_t, s.ka[kb]);
-            kbv = __builtin_bit_cast(bf16x8_t, s.kb[kb]);
+        for (int x = 0; x < 4; ++x) {
+            const u32x4_t kr = x < 2 ? s.ka[x] : s.kb[x - 2];
+            const bf16x8_t k0 = fp8x8(kr[0], kr[1]), k1 = fp8x8(kr[2], kr[3]);
+            f32x4_t d0 = {0.0f, 0.0f, 0.0f, 0.0f};
+            d0 = mma(k0, qh[0], d0);
+            d0 = mma(k1, qh[1], d0);
+            if constexpr (kHiLo) {
+                d0 = mma(k0, ql[0], d0);
+                d0 = mma(k1, ql[1], d0);
+            }
+            f32x4_t d1 = d0;
+            if constexpr (kSets == 2) {
+                d1 = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+                d1 = mma(k0, qh[2], d1);
+                d1 = mma(k1, qh[3], d1);
+                if constexpr (kHiLo) {
+                    d1 = mma(k0, ql[2], d1);
+                    d1 = mma(k1, ql[3], d1);
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const float own = upper ? d1[2 * e + 1] : d0[2 * e];
+                const float send = upper ? d0[2 * e + 1] : d1[2 * e];
+                sc[2 * x + e] = (own + row_ror8(send)) * ks[2 * x + e];
+            }
         }
-        sa = mma(ka, qh[kb], sa);
-        sb = mma(kbv, qh[kb], sb);
-        if constexpr (kHiLo) {
-            sa = mma(ka, ql[kb], sa);
-            sb = mma(kbv, ql[kb], sb);
+    } else {
+        f32x4_t sa = {0.0f, 0.0f, 0.0f, 0.0f}, sb = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int kb = 0; kb < 2 * C; ++kb) {
+            bf16x8_t ka, kbv;
+            if constexpr (ES == 1) {
+                const int c = kb >> 1, half = kb & 1;
+                ka = fp8x8(s.ka[c][2 * half], s.ka[c][2 * half + 1]);
+                kbv = fp8x8(s.kb[c][2 * half], s.kb[c][2 * half + 1]);
+            } else {
+                ka = __builtin_bit_cast(bf16x8_t, s.ka[kb]);
+                kbv = __builtin_bit_cast(bf16x8_t, s.kb[kb]);
+            }
+            sa = mma(ka, qh[kb], sa);
+            sb = mma(kbv, qh[kb], sb);
+            if constexpr (kHiLo) {
+                sa = mma(ka, ql[kb], sa);
+                sb = mma(kbv, ql[kb], sb);
+            }
         }
-    }
-    float sc[8] = {sa[0] * ks_a.x, sa[1] * ks_a.y, sa[2] * ks_a.z, sa[3] * ks_a.w,
-                   sb[0] * ks_b.x, sb[1] * ks_b.y, sb[2] * ks_b.z, sb[3] * ks_b.w};
-    if (!full) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            if (4 * j + i >= lim_a) sc[i] = kNegInf;
-            if (4 * j + i >= lim_b) sc[4 + i] = kNegInf;
+            sc[i] = sa[i] * ks[i];
+            sc[4 + i] = sb[i] * ks[4 + i];
         }
+    }
+    bool live[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) live[i] = full || step_token<kWL>(i, j) < (i < 4 ? lim_a : lim_b);
+    if (!full) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (!live[i]) sc[i] = kNegInf;
     }
 
     // Online softmax over the 32 tokens (8 per lane, 4 lane groups per column).
@@ -292,7 +413,6 @@ __device__ __forceinline__ void compute_step(WaveState<C>& st, const StepData<C,
         for (int nb = 0; nb < 4 * C; ++nb) st.o[nb] *= alpha;
     }
     st.m = m_new;
-    const float vs[8] = {vs_a.x, vs_a.y, vs_a.z, vs_a.w, vs_b.x, vs_b.y, vs_b.z, vs_b.w};
     float pv[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -302,10 +422,8 @@ __device__ __forceinline__ void compute_step(WaveState<C>& st, const StepData<C,
     }
     if (!full) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            if (4 * j + i >= lim_a) pv[i] = 0.0f;
-            if (4 * j + i >= lim_b) pv[4 + i] = 0.0f;
-        }
+        for (int i = 0; i < 8; ++i)
+            if (!live[i]) pv[i] = 0.0f;
     }
     bf16x8_t ph, pl;
 #pragma unroll
@@ -318,9 +436,8 @@ __device__ __forceinline__ void compute_step(WaveState<C>& st, const StepData<C,
     uint32_t vr[8][VW];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const bool live = full || (4 * j + (i & 3) < (i < 4 ? lim_a : lim_b));
 #pragma unroll
-        for (int c = 0; c < VW; ++c) vr[i][c] = live ? s.v[i][c] : 0u;
+        for (int c = 0; c < VW; ++c) vr[i][c] = live[i] ? s.v[i][c] : 0u;
     }
     if constexpr (ES == 1) {
         // Byte transpose: pair the codes of rows (2p, 2p + 1) at one column, widen.
@@ -358,7 +475,7 @@ __device__ __forceinline__ void compute_step(WaveState<C>& st, const StepData<C,
     }
 }
 
-template <int C, int QT, int ES>
+template <int C, int QT, int ES, int kSets>
 __global__ void __launch_bounds__(kMaxThreads)
 decode_mfma_kernel(MfmaArgs a) {
     constexpr int D = 64 * C;
@@ -426,16 +543,17 @@ decode_mfma_kernel(MfmaArgs a) {
                 if (T + 2 < t1) issue(buf1, T + 2, r1a, r1b);
             }
 
-            // Q^T operand of this head's G query heads (columns g >= G are zero),
+            // Q^T operands of this head's G query heads (heads g >= G are zero),
             // loaded while the first KV steps are in flight.
             bf16x8_t qh[2 * C], ql[2 * C];
-            const int hq = h * G + m16;
+            const int hq = h * G + m16;     // output column of this lane
             const bool qlive = m16 < G;
 #pragma unroll
             for (int kb = 0; kb < 2 * C; ++kb) {
+                const int g = qk_head<C, ES>(kb, m16);
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
-                    const float x = qlive ? load_q<QT>(a.d, b, hq, qk_dim<ES>(kb, j, i)) : 0.0f;
+                    const float x = g < G ? load_q<QT>(a.d, b, h * G + g, qk_dim<C, ES>(kb, m16, j, i)) : 0.0f;
                     const __bf16 hi = (__bf16)x;
                     qh[kb][i] = hi;
                     if constexpr (kHiLo) ql[kb][i] = (__bf16)(x - (float)hi);
@@ -446,7 +564,7 @@ decode_mfma_kernel(MfmaArgs a) {
                 const int64_t pos = (int64_t)tile0 * 16;
                 const int lim_a = ra.valid ? (int)max((int64_t)0, min((int64_t)16, len - pos)) : 0;
                 const int lim_b = rb.valid ? (int)max((int64_t)0, min((int64_t)16, len - pos - 16)) : 0;
-                compute_step<C, ES, kHiLo>(st, cur, qh, ql, stage, lane, lim_a, lim_b, a.d.score_scale);
+                compute_step<C, ES, kHiLo, kSets>(st, cur, qh, ql, stage, lane, lim_a, lim_b, a.d.score_scale);
             };
             if constexpr (ES == 1) {
                 while (true) {
@@ -620,7 +738,7 @@ int64_t max_groups(int32_t num_kv_heads) {
     return (int64_t)device_cus() * (per_cu > 0 ? per_cu : 1);
 }
 
-template <int C, int QT, int ES>
+template <int C, int QT, int ES, int kSets>
 hipError_t launch_c(const MfmaArgs& a, int64_t cap, hipStream_t s) {
     const int threads = 64 * waves_for(a.d.num_kv_heads);
     const size_t lds = (size_t)(a.d.batch + 1) * sizeof(int32_t);
@@ -631,14 +749,14 @@ hipError_t launch_c(const MfmaArgs& a, int64_t cap, hipStream_t s) {
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
     int& per_cu = resident[dev][threads / 64];
     if (per_cu == 0) {
-        const void* fn = reinterpret_cast<const void*>(&decode_mfma_kernel<C, QT, ES>);
+        const void* fn = reinterpret_cast<const void*>(&decode_mfma_kernel<C, QT, ES, kSets>);
         int n = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, threads, lds) != hipSuccess || n <= 0) n = 1;
         per_cu = n;
     }
     int64_t groups = (int64_t)device_cus() * per_cu;
     groups = groups < cap ? groups : cap;
-    const hipError_t err = launch_timed(decode_mfma_kernel<C, QT, ES>, dim3((unsigned)groups), dim3(threads), lds, s,
+    const hipError_t err = launch_timed(decode_mfma_kernel<C, QT, ES, kSets>, dim3((unsigned)groups), dim3(threads), lds, s,
                                         next_kernel_timing(), a);
     if (err != hipSuccess) return err;
     const int64_t pairs = (int64_t)a.d.batch * a.d.num_q_heads;
@@ -696,8 +814,11 @@ hipError_t launch_mfma_decode(const DecodeArgs& d, int kv_dtype, void* workspace
     a.part_acc = reinterpret_cast<float*>(ws + off[3]);
     const int64_t cap = max_groups(d.num_kv_heads);
     if (kv_dtype == KVFP8_BF16)
-        return d.head_dim == 64 ? launch_c<1, QT, 2>(a, cap, stream) : launch_c<2, QT, 2>(a, cap, stream);
-    return d.head_dim == 64 ? launch_c<1, QT, 1>(a, cap, stream) : launch_c<2, QT, 1>(a, cap, stream);
+        return d.head_dim == 64 ? launch_c<1, QT, 2, 1>(a, cap, stream) : launch_c<2, QT, 2, 1>(a, cap, stream);
+    if (d.head_dim == 64) return launch_c<1, QT, 1, 1>(a, cap, stream);
+    // Whole-row K layout: q heads 8..15 of a group need the second QK set.
+    return d.num_q_heads / d.num_kv_heads > 8 ? launch_c<2, QT, 1, 2>(a, cap, stream)
+                                               : launch_c<2, QT, 1, 1>(a, cap, stream);
 }
 
 template hipError_t launch_mfma_decode<KVFP8_F32>(const DecodeArgs&, int, void*, hipStream_t);

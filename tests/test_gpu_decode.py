@@ -84,7 +84,7 @@ def oracle_decode(q, cache, block_table, slots, lengths, rows=None):
 @t.inference_mode()
 @pytest.mark.parametrize("q_dtype", [t.float32, t.float16, t.bfloat16])
 @pytest.mark.parametrize("head_dim", [16, 64, 80, 128])
-@pytest.mark.parametrize("num_q_heads,num_kv_heads", [(8, 2), (4, 4), (32, 8), (64, 8)])
+@pytest.mark.parametrize("num_q_heads,num_kv_heads", [(8, 2), (4, 4), (32, 8), (64, 8), (24, 2), (16, 1)])
 def test_fp8_decode_matches_attention_over_dequantized_cache(q_dtype, head_dim, num_q_heads, num_kv_heads):
     block_size = 16
     num_blocks = sum(-(-n // 16) for n in DECODE_LENGTHS) + 4
