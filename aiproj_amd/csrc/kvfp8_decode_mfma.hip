@@ -69,6 +69,7 @@ struct MfmaArgs {
     float* part_m;       // [2 * max_groups, Hq]
     float* part_l;       // [2 * max_groups, Hq]
     float* part_acc;     // [2 * max_groups, Hq, D]
+    int32_t q_vec;       // q rows start 16-byte aligned: 8 elements per vector load
 };
 
 __device__ __forceinline__ int32_t uniform(int32_t x) { return __builtin_amdgcn_readfirstlane(x); }
@@ -161,9 +162,15 @@ struct TileRef {
     int32_t valid;
 };
 
+typedef const __attribute__((address_space(4))) int32_t* const_i32_ptr;
+
 __device__ __forceinline__ TileRef tile_ref(const MfmaArgs& a, const int32_t* table_row, int32_t tile) {
+    // The block table is read-only during the kernel and the address is
+    // wave-uniform: read it with a scalar load, whose wait (lgkmcnt) does not
+    // also wait for the K/V loads in flight the way a vector load's would.
     const int32_t page = tile >> a.tps_shift;
-    const int64_t phys = table_row[page];
+    const int64_t addr = uniform64((int64_t)(uintptr_t)(table_row + page));
+    const int64_t phys = *(const_i32_ptr)(uintptr_t)addr;
     const bool ok = phys >= 0 && phys < a.d.num_blocks;
     const int32_t base = (tile & ((1 << a.tps_shift) - 1)) << 4;
     TileRef r;
@@ -274,6 +281,79 @@ __device__ __forceinline__ int qk_dim(int kb, int c, int j, int i) {
 }
 
 // kSets = 2: whole-row K with G > 8 (a second set of QK products for heads 8..15).
+// Raw q elements of the Q^T operands of lane (c = l % 16, j = l / 16) for the G
+// q heads of KV head h of sequence b: operand kb holds q[b, h G + g, d .. d + 7]
+// with g = qk_head(kb, c), d = qk_dim(kb, c, j, 0) (16 or 32 bytes). Operands
+// whose heads are all >= G are not loaded (kOps of them are). Loads are 16 bytes
+// wide when q allows them (MfmaArgs::q_vec), else element loads.
+template <int C, int QT>
+struct QRaw {
+    static constexpr int kWords = QT == KVFP8_F32 ? 8 : 4;
+    uint32_t w[2 * C][kWords];
+};
+
+template <int C, int ES, int QT, int kOps>
+__device__ __forceinline__ void load_q_raw(const MfmaArgs& a, int b, int h, int G, int lane, QRaw<C, QT>& r) {
+    using T = typename Elem<QT>::T;
+    constexpr int kWords = QRaw<C, QT>::kWords;
+    const int c = lane & 15, j = lane >> 4;
+    const T* base = reinterpret_cast<const T*>(a.d.q) + (int64_t)b * a.d.q_stride_b;
+    const T* p[kOps];
+#pragma unroll
+    for (int kb = 0; kb < kOps; ++kb) {
+        const int g = min(qk_head<C, ES>(kb, c), G - 1);
+        p[kb] = base + (int64_t)(h * G + g) * a.d.q_stride_h + qk_dim<C, ES>(kb, c, j, 0);
+    }
+    if (a.q_vec) {
+#pragma unroll
+        for (int kb = 0; kb < kOps; ++kb) {
+#pragma unroll
+            for (int v = 0; v < kWords / 4; ++v) {
+                const u32x4_t u = *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const uint8_t*>(p[kb]) + 16 * v);
+                r.w[kb][4 * v] = u.x;
+                r.w[kb][4 * v + 1] = u.y;
+                r.w[kb][4 * v + 2] = u.z;
+                r.w[kb][4 * v + 3] = u.w;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int kb = 0; kb < kOps; ++kb) {
+            if constexpr (QT == KVFP8_F32) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) r.w[kb][i] = __builtin_bit_cast(uint32_t, p[kb][i]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) r.w[kb][i] = (uint32_t)p[kb][2 * i] | ((uint32_t)p[kb][2 * i + 1] << 16);
+            }
+        }
+    }
+}
+
+// Q^T operands from the raw elements: bf16 (f32 and f16 q as hi + lo parts),
+// zero for heads g >= G and for operands not loaded.
+template <int C, int ES, int QT, int kOps, bool kHiLo>
+__device__ __forceinline__ void q_operands(const QRaw<C, QT>& r, int G, int lane, bf16x8_t* qh, bf16x8_t* ql) {
+    using T = typename Elem<QT>::T;
+    const int c = lane & 15;
+#pragma unroll
+    for (int kb = 0; kb < 2 * C; ++kb) {
+        const bool live = kb < kOps && qk_head<C, ES>(kb, c) < G;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            float x = 0.0f;
+            if (kb < kOps) {
+                if constexpr (QT == KVFP8_F32) x = __builtin_bit_cast(float, r.w[kb][i]);
+                else x = Elem<QT>::load((T)((r.w[kb][i >> 1] >> (16 * (i & 1))) & 0xFFFFu));
+            }
+            x = live ? x : 0.0f;
+            const __bf16 hi = (__bf16)x;
+            qh[kb][i] = hi;
+            if constexpr (kHiLo) ql[kb][i] = (__bf16)(x - (float)hi);
+        }
+    }
+}
+
 template <int C, int ES, bool kHiLo, int kSets>
 __device__ __forceinline__ void compute_step(WaveState<C>& st, const StepData<C, ES>& s, const bf16x8_t* qh,
                                              const bf16x8_t* ql, float4* stage, int lane, int lim_a,
@@ -530,6 +610,15 @@ decode_mfma_kernel(MfmaArgs a) {
             // Load pipeline: e4m3fn keeps the loads of steps T + 2 and T + 4 in
             // flight while step T is computed (three buffers); bf16 steps are twice
             // the bytes and keep one step in flight (two buffers).
+            // Q^T operands of this head's G query heads: loads issued before the
+            // first K/V loads, converted after them, so that the first step waits
+            // for nothing else.
+            constexpr int kQOps = kWholeRowK<C, ES> ? 2 * kSets : 2 * C;
+            QRaw<C, QT> qraw;
+            load_q_raw<C, ES, QT, kQOps>(a, b, h, G, lane, qraw);
+            const int hq = h * G + m16;     // output column of this lane
+            const bool qlive = m16 < G;
+
             StepData<C, ES> buf0, buf1, buf2;
             TileRef r0a, r0b, r1a, r1b, r2a, r2b;
             auto issue = [&](StepData<C, ES>& dst, int32_t tile0, TileRef& ra, TileRef& rb) {
@@ -542,23 +631,9 @@ decode_mfma_kernel(MfmaArgs a) {
             if constexpr (ES == 1) {
                 if (T + 2 < t1) issue(buf1, T + 2, r1a, r1b);
             }
-
-            // Q^T operands of this head's G query heads (heads g >= G are zero),
-            // loaded while the first KV steps are in flight.
             bf16x8_t qh[2 * C], ql[2 * C];
-            const int hq = h * G + m16;     // output column of this lane
-            const bool qlive = m16 < G;
-#pragma unroll
-            for (int kb = 0; kb < 2 * C; ++kb) {
-                const int g = qk_head<C, ES>(kb, m16);
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const float x = g < G ? load_q<QT>(a.d, b, h * G + g, qk_dim<C, ES>(kb, m16, j, i)) : 0.0f;
-                    const __bf16 hi = (__bf16)x;
-                    qh[kb][i] = hi;
-                    if constexpr (kHiLo) ql[kb][i] = (__bf16)(x - (float)hi);
-                }
-            }
+            q_operands<C, ES, QT, kQOps, kHiLo>(qraw, G, lane, qh, ql);
+
 
             auto compute = [&](const StepData<C, ES>& cur, int32_t tile0, const TileRef& ra, const TileRef& rb) {
                 const int64_t pos = (int64_t)tile0 * 16;
@@ -812,6 +887,8 @@ hipError_t launch_mfma_decode(const DecodeArgs& d, int kv_dtype, void* workspace
     a.part_m = reinterpret_cast<float*>(ws + off[1]);
     a.part_l = reinterpret_cast<float*>(ws + off[2]);
     a.part_acc = reinterpret_cast<float*>(ws + off[3]);
+    const int64_t qsize = QT == KVFP8_F32 ? 4 : 2;
+    a.q_vec = ((uintptr_t)d.q % 16 == 0 && (d.q_stride_b * qsize) % 16 == 0 && (d.q_stride_h * qsize) % 16 == 0) ? 1 : 0;
     const int64_t cap = max_groups(d.num_kv_heads);
     if (kv_dtype == KVFP8_BF16)
         return d.head_dim == 64 ? launch_c<1, QT, 2, 1>(a, cap, stream) : launch_c<2, QT, 2, 1>(a, cap, stream);
