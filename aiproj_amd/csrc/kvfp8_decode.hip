@@ -285,7 +285,8 @@ namespace {
 template <int QT>
 hipError_t dispatch_kv(const DecodeArgs& a, int kv_dtype, const Plan& p, void* workspace, hipStream_t s) {
     const bool aligned = (((uintptr_t)a.k_cache | (uintptr_t)a.v_cache) & 15) == 0;
-    if (p.mfma && aligned) return launch_mfma_decode<QT>(a, kv_dtype, workspace, s);
+    // The MFMA kernel keeps slot * 32 + count per sequence in an int32.
+    if (p.mfma && aligned && a.bt_rows < ((int64_t)1 << 26)) return launch_mfma_decode<QT>(a, kv_dtype, workspace, s);
     const int64_t units_total = (int64_t)a.batch * p.max_chunks * a.num_q_heads;
     hipError_t err;
     switch (kv_dtype) {

@@ -60,7 +60,7 @@ constexpr int kMaxWaves = 8;            // KV heads served by one workgroup at a
 constexpr int kMaxThreads = 64 * kMaxWaves;
 constexpr int kMinTilesPerGroup = 8;    // a workgroup gets at least 128 tokens per head
 constexpr int kWavesPerCu = 16;         // target waves resident per CU (caps the grid)
-constexpr int kMfmaMaxBatch = 8191;     // LDS tile prefix of (batch + 1) int32
+constexpr int kMfmaMaxBatch = 8191;     // LDS: tile prefix (batch + 1) and sequence metadata (batch) int32
 
 struct MfmaArgs {
     DecodeArgs d;
@@ -121,9 +121,11 @@ __device__ __forceinline__ int step_token(int i, int j) {
     else return 4 * j + (i & 3);
 }
 
-// Tile prefix over the batch in LDS: prefix[b] = sum_{i<b} ceil(len_i / 16).
-// Per-thread runs, a shuffle scan inside each wave, then the wave totals.
-__device__ void build_tile_prefix(const DecodeArgs& a, int32_t* prefix, int32_t* wave_total) {
+// Tile prefix over the batch in LDS: prefix[b] = sum_{i<b} ceil(len_i / 16),
+// and meta[b] = slot_b * 32 + (tokens in the last tile of b) for sequences with
+// tokens (slots are below 2^26, checked by the host). Per-thread runs, a shuffle
+// scan inside each wave, then the wave totals.
+__device__ void build_tile_prefix(const DecodeArgs& a, int32_t* prefix, int32_t* meta, int32_t* wave_total) {
     const int threads = blockDim.x, tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int per = (a.batch + threads - 1) / threads;
@@ -133,8 +135,11 @@ __device__ void build_tile_prefix(const DecodeArgs& a, int32_t* prefix, int32_t*
         const int b = begin + i;
         if (b < a.batch) {
             int64_t slot;
+            const int64_t len = seq_tokens(a, b, &slot);
+            const int32_t tiles = (int32_t)((len + 15) >> 4);
             prefix[b] = local;
-            local += (int32_t)((seq_tokens(a, b, &slot) + 15) >> 4);
+            meta[b] = tiles > 0 ? (int32_t)(slot << 5) | (int32_t)(len - 16 * (int64_t)(tiles - 1)) : 0;
+            local += tiles;
         }
     }
     int32_t incl = local;
@@ -561,11 +566,12 @@ decode_mfma_kernel(MfmaArgs a) {
     constexpr int D = 64 * C;
     constexpr int NB = 4 * C;
     constexpr bool kHiLo = QT != KVFP8_BF16;
-    extern __shared__ int32_t prefix[];                // [batch + 1]
+    extern __shared__ int32_t prefix[];                // [batch + 1], then meta [batch]
     __shared__ int32_t wave_total[kMaxWaves];
     __shared__ float4 stage_all[kMaxWaves][16];
 
-    build_tile_prefix(a.d, prefix, wave_total);
+    int32_t* meta = prefix + a.d.batch + 1;
+    build_tile_prefix(a.d, prefix, meta, wave_total);
     const int32_t total = prefix[a.d.batch];
     const int32_t want = (total + kMinTilesPerGroup - 1) / kMinTilesPerGroup;
     const int32_t groups = min((int32_t)gridDim.x, max(want, 1));
@@ -596,9 +602,10 @@ decode_mfma_kernel(MfmaArgs a) {
             const int32_t t0 = tile - seq0, t1 = seg1 - seq0;
             const bool whole = tile == seq0 && seg1 == seq1;
             const int slot_index = 2 * w + (start >= seq0 ? 0 : 1);
-            int64_t slot;
-            const int64_t len = uniform64(seq_tokens(a.d, b, &slot));
-            slot = uniform64(slot);
+            // Slot and length from the LDS metadata (the segment has tiles).
+            const int32_t mt = uniform(meta[b]);
+            const int64_t slot = mt >> 5;
+            const int64_t len = 16 * (int64_t)(seq1 - seq0 - 1) + (mt & 31);
             const int32_t* table_row = a.d.block_table + slot * a.d.bt_width;
 
             WaveState<C> st;
@@ -816,20 +823,31 @@ int64_t max_groups(int32_t num_kv_heads) {
 template <int C, int QT, int ES, int kSets>
 hipError_t launch_c(const MfmaArgs& a, int64_t cap, hipStream_t s) {
     const int threads = 64 * waves_for(a.d.num_kv_heads);
-    const size_t lds = (size_t)(a.d.batch + 1) * sizeof(int32_t);
-    // Resident workgroups per CU, queried once per (device, workgroup size); the
-    // dynamic LDS (<= 32 KiB) never limits residency at these sizes.
+    const size_t lds = (size_t)(2 * a.d.batch + 1) * sizeof(int32_t);
+    // Resident workgroups per CU: the register limit, queried once per (device,
+    // workgroup size) without dynamic LDS, capped by what the batch-sized LDS
+    // (up to 64 KiB) leaves room for. Only a sizing choice: the work split is
+    // correct for any grid.
     static int resident[64][kMaxWaves + 1] = {};     // per template instance
+    static int lds_per_cu[64] = {};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
     int& per_cu = resident[dev][threads / 64];
     if (per_cu == 0) {
         const void* fn = reinterpret_cast<const void*>(&decode_mfma_kernel<C, QT, ES, kSets>);
         int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, threads, lds) != hipSuccess || n <= 0) n = 1;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, threads, 0) != hipSuccess || n <= 0) n = 1;
         per_cu = n;
     }
-    int64_t groups = (int64_t)device_cus() * per_cu;
+    if (lds_per_cu[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess || n <= 0)
+            n = 64 * 1024;
+        lds_per_cu[dev] = n;
+    }
+    const int64_t by_lds = (int64_t)lds_per_cu[dev] / (int64_t)(lds + 4096);   // + static LDS
+    const int64_t fit = by_lds < per_cu ? by_lds : per_cu;
+    int64_t groups = (int64_t)device_cus() * (fit > 0 ? fit : 1);
     groups = groups < cap ? groups : cap;
     const hipError_t err = launch_timed(decode_mfma_kernel<C, QT, ES, kSets>, dim3((unsigned)groups), dim3(threads), lds, s,
                                         next_kernel_timing(), a);
