@@ -45,6 +45,8 @@ SIGNATURES = {
     "kvfp8_add_rmsnorm_forward": (_INT, [_P, _P, _INT, _I64, _I64, _I64, _I32, _P, _INT, ctypes.c_float,
                                          _P, _I64, _P, _I64, _P, _P]),
     "kvfp8_rope_inplace": (_INT, [_P, _INT, _I64, _I32, _I32, _I64, _I64, _P, _INT, _P, _P, _INT, _I64, _P]),
+    "kvfp8_prefill_attention": (_INT, [_P, _P, _P, _INT, _I64, _I32, _I32, _I32, _P, _INT, _I32, _I32,
+                                       ctypes.c_float, _P, _P, _P]),
     "kvfp8_timing_enable": (_INT, [_I32]),
     "kvfp8_timing_read": (_INT, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I64)]),
     "kvfp8_strerror": (ctypes.c_char_p, [_INT]),

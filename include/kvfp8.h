@@ -150,6 +150,24 @@ int kvfp8_add_rmsnorm_forward(const void* x_dev, const void* update_dev, int dty
                               void* out_dev, int64_t out_stride, float* inv_rms_dev, void* stream);
 
 /*
+ * Varlen causal attention over packed prompts (prefill):
+ *   q [T, Hq, D], k and v [T, Hkv, D] contiguous, one dtype (f32/f16/bf16);
+ *   cu_seqlens [batch + 1] (int32/int64): sequence b is tokens
+ *   [cu_seqlens[b], cu_seqlens[b + 1]); query row i of it attends keys 0..i of it;
+ *   q head h reads KV head h / (Hq / Hkv).
+ *   out [T, Hq, D] (q's dtype) and lse [T, Hq] float32 = m + log(sum exp(s - m)) of
+ *   the scaled scores s = scale * q.k. Rows outside every sequence are not written;
+ *   only the first max_seq_len rows of each sequence are computed.
+ *   head_dim: multiple of 8, at most 128. Pointers 16-byte aligned.
+ * Replaces the forward of reference src/torch_llm/kernals/flash_attention.py:51-211
+ * (flash_attention_forward and flash_attention_forward_kernal).
+ */
+int kvfp8_prefill_attention(const void* q_dev, const void* k_dev, const void* v_dev, int dtype,
+                            int64_t total_tokens, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                            const void* cu_seqlens_dev, int cu_dtype, int32_t batch, int32_t max_seq_len,
+                            float scale, void* out_dev, float* lse_dev, void* stream);
+
+/*
  * Interleaved-pair rotary embedding in place on heads [0, heads) of every row of x
  * (element strides row_stride, head_stride; pairs (2i, 2i+1) of head_dim):
  *   x0' = c x0 - s x1, x1' = s x0 + c x1,  c/s = cos/sin_table[positions[r], i]

@@ -11,6 +11,8 @@ The oracle restates, in numpy, the reference's own test oracle:
   * `decode_one`      - reference `tests/test_kv_cache_quantization.py:440-446`
   * `paged_decode`    - the per-row stack at `tests/test_kv_cache_quantization.py:475-478`
   * `scatter_append`  - address math of `kernals/kv_cache/quantized_append.py:103-105`
+  * `causal_varlen_attention` - the ragged reference of `tests/test_flash_attention.py:44-85`
+    and the lse of `kernals/flash_attention.py:205-210`
 and the page-table gather of `inference/page_allocator.py:225-245`.
 """
 
@@ -26,6 +28,7 @@ from .kvfp8 import (  # noqa: F401
     paged_history,
     decode_one,
     paged_decode,
+    causal_varlen_attention,
     decode_algorithmic_bytes,
     append_algorithmic_bytes,
 )

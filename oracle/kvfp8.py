@@ -213,6 +213,44 @@ def paged_decode(q, k_cache, v_cache, k_scales, v_scales, block_table, slots, co
     return np.stack(rows) if rows else np.zeros(q.shape, dtype=np.float64)
 
 
+def causal_varlen_attention(q, k, v, cu_seqlens, max_seq_len, scale):
+    """Packed causal attention in float64 -> (out [T, H_q, D], lse [T, H_q]).
+
+    Reference `tests/test_flash_attention.py:44-85` (the ragged PyTorch reference: per
+    sequence, `softmax(scale q k^T)` under a lower-triangular mask, KV heads repeated
+    per query group) and the kernel's outputs at `kernals/flash_attention.py:205-210`:
+    `lse = max + log(sum exp(s - max))` of the scaled scores. Only the first
+    `max_seq_len` rows of each sequence are produced (the reference grid covers
+    `cdiv(batch_max_seq_len, BLOCK_M)` query blocks); every other row is NaN.
+    """
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    total, num_q_heads, head_dim = q.shape
+    group = num_q_heads // k.shape[1]
+    out = np.full(q.shape, np.nan)
+    lse = np.full((total, num_q_heads), np.nan)
+    bounds = [int(x) for x in cu_seqlens]
+    for b in range(len(bounds) - 1):
+        s0, s1 = bounds[b], bounds[b + 1]
+        n = min(s1 - s0, int(max_seq_len))
+        if n <= 0:
+            continue
+        length = s1 - s0
+        qs = np.transpose(q[s0:s0 + n], (1, 0, 2))                                     # [H_q, n, D]
+        ks = np.repeat(np.transpose(k[s0:s1], (1, 0, 2)), group, axis=0)               # [H_q, L, D]
+        vs = np.repeat(np.transpose(v[s0:s1], (1, 0, 2)), group, axis=0)
+        scores = scale * np.matmul(qs, np.transpose(ks, (0, 2, 1)))                    # [H_q, n, L]
+        mask = np.arange(length)[None, :] <= np.arange(n)[:, None]
+        scores = np.where(mask[None], scores, -np.inf)
+        mx = scores.max(axis=-1, keepdims=True)
+        weights = np.exp(scores - mx)
+        total_w = weights.sum(axis=-1, keepdims=True)
+        out[s0:s0 + n] = np.transpose(np.matmul(weights / total_w, vs), (1, 0, 2))
+        lse[s0:s0 + n] = np.transpose((mx + np.log(total_w))[..., 0], (1, 0))
+    return out, lse
+
+
 # ---------------------------------------------------------------------------
 # Algorithmic byte counts (the roofline numerators).
 # ---------------------------------------------------------------------------

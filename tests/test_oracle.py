@@ -299,3 +299,83 @@ def test_algorithmic_bytes_north_star():
     nbytes = oracle.decode_algorithmic_bytes([4096] * 32, 32, 8, 128, 16)
     assert nbytes == 32 * 4096 * 8 * 264 + 2 * 32 * 32 * 128 * 2 + 32 * 256 * 4
     assert abs(nbytes / 1e6 - 277.4) < 0.1
+
+
+# ---------------------------------------------------------------------------
+# Causal varlen (prefill) attention
+# ---------------------------------------------------------------------------
+
+def _packed(rng, lengths, hq, hkv, d):
+    total = sum(lengths)
+    q = rng.standard_normal((total, hq, d))
+    k = rng.standard_normal((total, hkv, d))
+    v = rng.standard_normal((total, hkv, d))
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int64)
+    return q, k, v, cu
+
+
+def test_prefill_oracle_matches_brute_force_loops():
+    rng = np.random.default_rng(21)
+    lengths = [1, 4, 6]
+    hq, hkv, d = 4, 2, 3
+    q, k, v, cu = _packed(rng, lengths, hq, hkv, d)
+    scale = 0.7
+    out, lse = oracle.causal_varlen_attention(q, k, v, cu, max(lengths), scale)
+    for b, n in enumerate(lengths):
+        s0 = int(cu[b])
+        for i in range(n):
+            for h in range(hq):
+                kv = h // (hq // hkv)
+                s = [scale * sum(q[s0 + i, h, e] * k[s0 + t_, kv, e] for e in range(d)) for t_ in range(i + 1)]
+                mx = max(s)
+                w = [math.exp(x - mx) for x in s]
+                tot = sum(w)
+                for e in range(d):
+                    expected = sum(w[t_] * v[s0 + t_, kv, e] for t_ in range(i + 1)) / tot
+                    assert abs(out[s0 + i, h, e] - expected) < 1e-12
+                assert abs(lse[s0 + i, h] - (mx + math.log(tot))) < 1e-12
+
+
+def test_prefill_oracle_matches_torch_sdpa():
+    rng = np.random.default_rng(22)
+    lengths = [3, 73, 141]                 # the reference test's ragged batch
+    hq, hkv, d = 8, 2, 16
+    q, k, v, cu = _packed(rng, lengths, hq, hkv, d)
+    scale = 1.0 / math.sqrt(d)
+    out, lse = oracle.causal_varlen_attention(q, k, v, cu, max(lengths), scale)
+    for b, n in enumerate(lengths):
+        s0 = int(cu[b])
+        qs = t.from_numpy(q[s0:s0 + n]).transpose(0, 1)
+        ks = t.from_numpy(k[s0:s0 + n]).transpose(0, 1).repeat_interleave(hq // hkv, 0)
+        vs = t.from_numpy(v[s0:s0 + n]).transpose(0, 1).repeat_interleave(hq // hkv, 0)
+        ref = t.nn.functional.scaled_dot_product_attention(qs, ks, vs, is_causal=True, scale=scale)
+        np.testing.assert_allclose(out[s0:s0 + n], ref.transpose(0, 1).numpy(), rtol=1e-10, atol=1e-10)
+        scores = scale * (qs @ ks.transpose(-1, -2))
+        scores = scores.masked_fill(t.ones(n, n, dtype=t.bool).triu(1), float("-inf"))
+        np.testing.assert_allclose(lse[s0:s0 + n], t.logsumexp(scores, -1).transpose(0, 1).numpy(),
+                                   rtol=1e-10, atol=1e-10)
+
+
+def test_prefill_oracle_invariants():
+    rng = np.random.default_rng(23)
+    lengths = [5, 0, 9]
+    hq, hkv, d = 6, 3, 4
+    q, k, v, cu = _packed(rng, lengths, hq, hkv, d)
+    out, lse = oracle.causal_varlen_attention(q, k, v, cu, 9, 0.5)
+    # Row 0 of a sequence attends only itself: its output is its own V row.
+    for b in (0, 2):
+        s0 = int(cu[b])
+        for h in range(hq):
+            np.testing.assert_allclose(out[s0, h], v[s0, h // 2], rtol=1e-13)
+            assert abs(lse[s0, h] - 0.5 * float(q[s0, h] @ k[s0, h // 2])) < 1e-12
+    # Causality: changing later tokens leaves earlier rows unchanged.
+    k2, v2 = k.copy(), v.copy()
+    k2[cu[2] + 6:] += 3.0
+    v2[cu[2] + 6:] -= 2.0
+    out2, _ = oracle.causal_varlen_attention(q, k2, v2, cu, 9, 0.5)
+    np.testing.assert_array_equal(out2[: cu[2] + 6], out[: cu[2] + 6])
+    assert not np.allclose(out2[cu[2] + 6:], out[cu[2] + 6:])
+    # Truncation at max_seq_len: rows past it are not produced.
+    out3, lse3 = oracle.causal_varlen_attention(q, k, v, cu, 4, 0.5)
+    assert np.isnan(out3[cu[0] + 4]).all() and np.isnan(lse3[cu[2] + 4:]).all()
+    np.testing.assert_array_equal(out3[cu[2]:cu[2] + 4], out[cu[2]:cu[2] + 4])
