@@ -32,15 +32,17 @@ _P = ctypes.c_void_p
 _I32 = ctypes.c_int32
 _I64 = ctypes.c_int64
 _INT = ctypes.c_int
+_DECODE_ARGS = [_P, _INT, _I64, _I64, _I32, _I32, _I32, _I32, _P, _P, _INT, _P, _P, _I64, _I32, _P, _I64, _I64,
+                _P, _INT, _P, _INT, ctypes.c_float, _P, _P, _I64, _P]
 SIGNATURES = {
     "kvfp8_quantize_append": (_INT, [_P, _P, _INT, _I64, _I64, _I64, _I64, _P, _INT, _P, _INT,
                                      _I64, _I32, _I32, _I64, _I32, _P, _P, _P, _P, _P]),
     "kvfp8_store_append": (_INT, [_P, _P, _INT, _I64, _I64, _I64, _I64, _P, _INT, _P, _INT,
                                   _I64, _I32, _I32, _I64, _I32, _P, _P, _INT, _P]),
     "kvfp8_decode_workspace_bytes": (_I64, [_I32, _I32, _I32, _I32, _I64, _I32, _INT]),
-    "kvfp8_paged_decode": (_INT, [_P, _INT, _I64, _I64, _I32, _I32, _I32, _I32, _P, _P, _INT,
-                                  _P, _P, _I64, _I32, _P, _I64, _I64, _P, _INT, _P, _INT,
-                                  ctypes.c_float, _P, _P, _I64, _P]),
+    "kvfp8_paged_decode": (_INT, _DECODE_ARGS),
+    "kvfp8_paged_decode_split": (_INT, _DECODE_ARGS),
+    "kvfp8_paged_decode_reduce": (_INT, _DECODE_ARGS),
     "kvfp8_rmsnorm_forward": (_INT, [_P, _INT, _I64, _I64, _I32, _P, _INT, ctypes.c_float, _P, _I64, _P, _P]),
     "kvfp8_add_rmsnorm_forward": (_INT, [_P, _P, _INT, _I64, _I64, _I64, _I32, _P, _INT, ctypes.c_float,
                                          _P, _I64, _P, _I64, _P, _P]),

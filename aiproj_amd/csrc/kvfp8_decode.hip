@@ -283,21 +283,33 @@ KernelTiming kvfp8::next_kernel_timing() {
 namespace {
 
 template <int QT>
-hipError_t dispatch_kv(const DecodeArgs& a, int kv_dtype, const Plan& p, void* workspace, hipStream_t s) {
+hipError_t dispatch_kv(const DecodeArgs& a, int kv_dtype, const Plan& p, void* workspace, hipStream_t s,
+                       int phases) {
     const bool aligned = (((uintptr_t)a.k_cache | (uintptr_t)a.v_cache) & 15) == 0;
     // The MFMA kernel keeps slot * 32 + count per sequence in an int32.
-    if (p.mfma && aligned && a.bt_rows < ((int64_t)1 << 26)) return launch_mfma_decode<QT>(a, kv_dtype, workspace, s);
-    const int64_t units_total = (int64_t)a.batch * p.max_chunks * a.num_q_heads;
-    hipError_t err;
-    switch (kv_dtype) {
-        case KVFP8_E4M3FN: err = launch_generic<KVFP8_E4M3FN, QT>(a, units_total, s); break;
-        case KVFP8_BF16: err = launch_generic<KVFP8_BF16, QT>(a, units_total, s); break;
-        case KVFP8_F16: err = launch_generic<KVFP8_F16, QT>(a, units_total, s); break;
-        default: err = launch_generic<KVFP8_F32, QT>(a, units_total, s); break;
+    if (p.mfma && aligned && a.bt_rows < ((int64_t)1 << 26))
+        return launch_mfma_decode<QT>(a, kv_dtype, workspace, s, phases);
+    if (phases & kPhaseSplit) {
+        const int64_t units_total = (int64_t)a.batch * p.max_chunks * a.num_q_heads;
+        hipError_t err;
+        switch (kv_dtype) {
+            case KVFP8_E4M3FN: err = launch_generic<KVFP8_E4M3FN, QT>(a, units_total, s); break;
+            case KVFP8_BF16: err = launch_generic<KVFP8_BF16, QT>(a, units_total, s); break;
+            case KVFP8_F16: err = launch_generic<KVFP8_F16, QT>(a, units_total, s); break;
+            default: err = launch_generic<KVFP8_F32, QT>(a, units_total, s); break;
+        }
+        if (err != hipSuccess) return err;
     }
-    if (err != hipSuccess) return err;
+    if (!(phases & kPhaseReduce)) return hipSuccess;
     return launch_combine<QT>(a, s);
 }
+
+int paged_decode(const void* q, int q_dtype, int64_t q_stride_b, int64_t q_stride_h, int32_t batch,
+                 int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, const void* k_cache,
+                 const void* v_cache, int kv_dtype, const float* k_scales, const float* v_scales,
+                 int64_t num_blocks, int32_t block_size, const int32_t* block_table, int64_t bt_rows,
+                 int64_t bt_width, const void* slots, int slots_dtype, const void* context_lengths, int ctx_dtype,
+                 float sm_scale, void* out, void* workspace, int64_t workspace_bytes, void* stream, int phases);
 
 }  // namespace
 
@@ -311,14 +323,40 @@ extern "C" int64_t kvfp8_decode_workspace_bytes(int32_t batch, int32_t num_q_hea
     return workspace_for(p, batch, num_q_heads, num_kv_heads, head_dim);
 }
 
-extern "C" int kvfp8_paged_decode(const void* q, int q_dtype, int64_t q_stride_b, int64_t q_stride_h,
-                                  int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
-                                  const void* k_cache, const void* v_cache, int kv_dtype,
-                                  const float* k_scales, const float* v_scales, int64_t num_blocks,
-                                  int32_t block_size, const int32_t* block_table, int64_t bt_rows,
-                                  int64_t bt_width, const void* slots, int slots_dtype,
-                                  const void* context_lengths, int ctx_dtype, float sm_scale, void* out,
-                                  void* workspace, int64_t workspace_bytes, void* stream) {
+// The three decode entry points share one argument list; they differ in which
+// of the two launches they enqueue.
+#define KVFP8_DECODE_PARAMS                                                                                  \
+    const void *q, int q_dtype, int64_t q_stride_b, int64_t q_stride_h, int32_t batch, int32_t num_q_heads,  \
+        int32_t num_kv_heads, int32_t head_dim, const void *k_cache, const void *v_cache, int kv_dtype,      \
+        const float *k_scales, const float *v_scales, int64_t num_blocks, int32_t block_size,                \
+        const int32_t *block_table, int64_t bt_rows, int64_t bt_width, const void *slots, int slots_dtype,   \
+        const void *context_lengths, int ctx_dtype, float sm_scale, void *out, void *workspace,              \
+        int64_t workspace_bytes, void *stream
+#define KVFP8_DECODE_ARGS                                                                                    \
+    q, q_dtype, q_stride_b, q_stride_h, batch, num_q_heads, num_kv_heads, head_dim, k_cache, v_cache,        \
+        kv_dtype, k_scales, v_scales, num_blocks, block_size, block_table, bt_rows, bt_width, slots,         \
+        slots_dtype, context_lengths, ctx_dtype, sm_scale, out, workspace, workspace_bytes, stream
+
+extern "C" int kvfp8_paged_decode(KVFP8_DECODE_PARAMS) {
+    return paged_decode(KVFP8_DECODE_ARGS, kPhaseSplit | kPhaseReduce);
+}
+
+extern "C" int kvfp8_paged_decode_split(KVFP8_DECODE_PARAMS) {
+    return paged_decode(KVFP8_DECODE_ARGS, kPhaseSplit);
+}
+
+extern "C" int kvfp8_paged_decode_reduce(KVFP8_DECODE_PARAMS) {
+    return paged_decode(KVFP8_DECODE_ARGS, kPhaseReduce);
+}
+
+namespace {
+
+int paged_decode(const void* q, int q_dtype, int64_t q_stride_b, int64_t q_stride_h, int32_t batch,
+                 int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, const void* k_cache,
+                 const void* v_cache, int kv_dtype, const float* k_scales, const float* v_scales,
+                 int64_t num_blocks, int32_t block_size, const int32_t* block_table, int64_t bt_rows,
+                 int64_t bt_width, const void* slots, int slots_dtype, const void* context_lengths, int ctx_dtype,
+                 float sm_scale, void* out, void* workspace, int64_t workspace_bytes, void* stream, int phases) {
     if (q_dtype != KVFP8_F32 && q_dtype != KVFP8_F16 && q_dtype != KVFP8_BF16) return KVFP8_EDTYPE;
     if (kv_dtype != KVFP8_E4M3FN && kv_dtype != KVFP8_BF16 && kv_dtype != KVFP8_F16 && kv_dtype != KVFP8_F32)
         return KVFP8_EDTYPE;
@@ -371,12 +409,14 @@ extern "C" int kvfp8_paged_decode(const void* q, int q_dtype, int64_t q_stride_b
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     hipError_t err;
     switch (q_dtype) {
-        case KVFP8_F32: err = dispatch_kv<KVFP8_F32>(a, kv_dtype, p, workspace, s); break;
-        case KVFP8_F16: err = dispatch_kv<KVFP8_F16>(a, kv_dtype, p, workspace, s); break;
-        default: err = dispatch_kv<KVFP8_BF16>(a, kv_dtype, p, workspace, s); break;
+        case KVFP8_F32: err = dispatch_kv<KVFP8_F32>(a, kv_dtype, p, workspace, s, phases); break;
+        case KVFP8_F16: err = dispatch_kv<KVFP8_F16>(a, kv_dtype, p, workspace, s, phases); break;
+        default: err = dispatch_kv<KVFP8_BF16>(a, kv_dtype, p, workspace, s, phases); break;
     }
     return (int)err;
 }
+
+}  // namespace
 
 extern "C" const char* kvfp8_strerror(int code) {
     switch (code) {

@@ -10,6 +10,12 @@
 namespace kvfp8 {
 
 constexpr float kLog2e = 1.4426950408889634f;
+
+// The two launches of one decode call: the split kernel (partial softmax states,
+// and the output rows of sequences it finishes whole) and the reduce kernel (the
+// merge of the partial states, zeros for empty sequences).
+constexpr int kPhaseSplit = 1;
+constexpr int kPhaseReduce = 2;
 constexpr float kNegInf = -__builtin_huge_valf();
 
 struct DecodeArgs {

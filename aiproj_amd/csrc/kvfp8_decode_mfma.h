@@ -15,7 +15,8 @@ bool mfma_decode_supported(int32_t batch, int32_t num_q_heads, int32_t num_kv_he
 int64_t mfma_workspace_layout(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                               int64_t offsets[4]);
 
+// phases: kPhaseSplit (the decode kernel), kPhaseReduce (the combine kernel), or both.
 template <int QT>
-hipError_t launch_mfma_decode(const DecodeArgs& a, int kv_dtype, void* workspace, hipStream_t stream);
+hipError_t launch_mfma_decode(const DecodeArgs& a, int kv_dtype, void* workspace, hipStream_t stream, int phases);
 
 }  // namespace kvfp8

@@ -15,6 +15,8 @@
 //
 // Inside a workgroup wave i serves KV head i (and i + waves, ...), so the
 // workgroup reads whole pages: 16 tokens x Hkv x D contiguous bytes of K and V.
+// The two waves that share a SIMD keep pace through an LDS step counter and the
+// wave issue priority (the arbiter would otherwise favour the older one).
 // One step of a wave covers two tiles (32 tokens) of its head:
 //
 //   scores   S^T[t, g] = K[t, :] . Q[g, :]      MFMA 16x16x32 bf16, A = K codes
@@ -569,6 +571,8 @@ decode_mfma_kernel(MfmaArgs a) {
     extern __shared__ int32_t prefix[];                // [batch + 1], then meta [batch]
     __shared__ int32_t wave_total[kMaxWaves];
     __shared__ float4 stage_all[kMaxWaves][16];
+    __shared__ int32_t progress[kMaxWaves];     // steps computed by each wave
+    if (threadIdx.x < kMaxWaves) progress[threadIdx.x] = 0;   // visible after the plan's barriers
 
     int32_t* meta = prefix + a.d.batch + 1;
     build_tile_prefix(a.d, prefix, meta, wave_total);
@@ -589,6 +593,21 @@ decode_mfma_kernel(MfmaArgs a) {
     const int m16 = lane & 15, j = lane >> 4;
     const int G = a.d.num_q_heads / a.d.num_kv_heads;
     float4* stage = stage_all[wave];
+
+    // Waves w and w + 4 share a SIMD, whose arbiter favours the older wave: left
+    // alone, waves 0-3 finish their (equal) work about 10% before waves 4-7 and the
+    // CU streams with half its waves for the rest of the range. After every step a
+    // wave publishes its step count and raises its issue priority while it is
+    // behind its partner, so both finish together.
+    const int partner = (wave ^ 4) < waves ? (wave ^ 4) : wave;
+    int32_t steps_done = 0;
+    auto keep_pace = [&]() {
+        ++steps_done;
+        if (lane == 0) *(volatile int32_t*)&progress[wave] = steps_done;
+        const int32_t other = uniform(*(volatile int32_t*)&progress[partner]);
+        if (steps_done < other) __builtin_amdgcn_s_setprio(2);
+        else __builtin_amdgcn_s_setprio(0);
+    };
 
     for (int h = wave; h < a.d.num_kv_heads; h += waves) {
         int32_t tile = start;
@@ -652,14 +671,17 @@ decode_mfma_kernel(MfmaArgs a) {
                 while (true) {
                     if (T + 4 < t1) issue(buf2, T + 4, r2a, r2b);
                     compute(buf0, T, r0a, r0b);
+                    keep_pace();
                     T += 2;
                     if (T >= t1) break;
                     if (T + 4 < t1) issue(buf0, T + 4, r0a, r0b);
                     compute(buf1, T, r1a, r1b);
+                    keep_pace();
                     T += 2;
                     if (T >= t1) break;
                     if (T + 4 < t1) issue(buf1, T + 4, r1a, r1b);
                     compute(buf2, T, r2a, r2b);
+                    keep_pace();
                     T += 2;
                     if (T >= t1) break;
                 }
@@ -667,10 +689,12 @@ decode_mfma_kernel(MfmaArgs a) {
                 while (true) {
                     if (T + 2 < t1) issue(buf1, T + 2, r1a, r1b);
                     compute(buf0, T, r0a, r0b);
+                    keep_pace();
                     T += 2;
                     if (T >= t1) break;
                     if (T + 2 < t1) issue(buf0, T + 2, r0a, r0b);
                     compute(buf1, T, r1a, r1b);
+                    keep_pace();
                     T += 2;
                     if (T >= t1) break;
                 }
@@ -821,7 +845,7 @@ int64_t max_groups(int32_t num_kv_heads) {
 }
 
 template <int C, int QT, int ES, int kSets>
-hipError_t launch_c(const MfmaArgs& a, int64_t cap, hipStream_t s) {
+hipError_t launch_c(const MfmaArgs& a, int64_t cap, hipStream_t s, int phases) {
     const int threads = 64 * waves_for(a.d.num_kv_heads);
     const size_t lds = (size_t)(2 * a.d.batch + 1) * sizeof(int32_t);
     // Resident workgroups per CU: the register limit, queried once per (device,
@@ -849,9 +873,12 @@ hipError_t launch_c(const MfmaArgs& a, int64_t cap, hipStream_t s) {
     const int64_t fit = by_lds < per_cu ? by_lds : per_cu;
     int64_t groups = (int64_t)device_cus() * (fit > 0 ? fit : 1);
     groups = groups < cap ? groups : cap;
-    const hipError_t err = launch_timed(decode_mfma_kernel<C, QT, ES, kSets>, dim3((unsigned)groups), dim3(threads), lds, s,
-                                        next_kernel_timing(), a);
-    if (err != hipSuccess) return err;
+    if (phases & kPhaseSplit) {
+        const hipError_t err = launch_timed(decode_mfma_kernel<C, QT, ES, kSets>, dim3((unsigned)groups), dim3(threads),
+                                            lds, s, next_kernel_timing(), a);
+        if (err != hipSuccess) return err;
+    }
+    if (!(phases & kPhaseReduce)) return hipSuccess;
     const int64_t pairs = (int64_t)a.d.batch * a.d.num_q_heads;
     hipLaunchKernelGGL((combine_mfma_kernel<C, QT>), dim3((unsigned)((pairs + 3) / 4)), dim3(256), 0, s, a);
     return hipGetLastError();
@@ -894,7 +921,7 @@ int64_t mfma_workspace_layout(int32_t batch, int32_t num_q_heads, int32_t num_kv
 }
 
 template <int QT>
-hipError_t launch_mfma_decode(const DecodeArgs& d, int kv_dtype, void* workspace, hipStream_t stream) {
+hipError_t launch_mfma_decode(const DecodeArgs& d, int kv_dtype, void* workspace, hipStream_t stream, int phases) {
     int64_t off[4];
     mfma_workspace_layout(d.batch, d.num_q_heads, d.num_kv_heads, d.head_dim, off);
     char* ws = reinterpret_cast<char*>(workspace);
@@ -909,15 +936,16 @@ hipError_t launch_mfma_decode(const DecodeArgs& d, int kv_dtype, void* workspace
     a.q_vec = ((uintptr_t)d.q % 16 == 0 && (d.q_stride_b * qsize) % 16 == 0 && (d.q_stride_h * qsize) % 16 == 0) ? 1 : 0;
     const int64_t cap = max_groups(d.num_kv_heads);
     if (kv_dtype == KVFP8_BF16)
-        return d.head_dim == 64 ? launch_c<1, QT, 2, 1>(a, cap, stream) : launch_c<2, QT, 2, 1>(a, cap, stream);
-    if (d.head_dim == 64) return launch_c<1, QT, 1, 1>(a, cap, stream);
+        return d.head_dim == 64 ? launch_c<1, QT, 2, 1>(a, cap, stream, phases)
+                                : launch_c<2, QT, 2, 1>(a, cap, stream, phases);
+    if (d.head_dim == 64) return launch_c<1, QT, 1, 1>(a, cap, stream, phases);
     // Whole-row K layout: q heads 8..15 of a group need the second QK set.
-    return d.num_q_heads / d.num_kv_heads > 8 ? launch_c<2, QT, 1, 2>(a, cap, stream)
-                                               : launch_c<2, QT, 1, 1>(a, cap, stream);
+    return d.num_q_heads / d.num_kv_heads > 8 ? launch_c<2, QT, 1, 2>(a, cap, stream, phases)
+                                               : launch_c<2, QT, 1, 1>(a, cap, stream, phases);
 }
 
-template hipError_t launch_mfma_decode<KVFP8_F32>(const DecodeArgs&, int, void*, hipStream_t);
-template hipError_t launch_mfma_decode<KVFP8_F16>(const DecodeArgs&, int, void*, hipStream_t);
-template hipError_t launch_mfma_decode<KVFP8_BF16>(const DecodeArgs&, int, void*, hipStream_t);
+template hipError_t launch_mfma_decode<KVFP8_F32>(const DecodeArgs&, int, void*, hipStream_t, int);
+template hipError_t launch_mfma_decode<KVFP8_F16>(const DecodeArgs&, int, void*, hipStream_t, int);
+template hipError_t launch_mfma_decode<KVFP8_BF16>(const DecodeArgs&, int, void*, hipStream_t, int);
 
 }  // namespace kvfp8

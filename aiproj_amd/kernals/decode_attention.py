@@ -13,7 +13,9 @@ The optional second calling form of the reference's planned state API (handoff D
 Unlike the reference wrapper, this one never synchronizes with the host: the split
 plan is built on the device inside the kernel (reference `:87-103` reads
 `cum_splits[-1].item()`), and no dummy scale tensors are allocated for plain caches.
-The work is two launches through the C ABI `kvfp8_paged_decode` (include/kvfp8.h).
+The work is two launches through the C ABI `kvfp8_paged_decode` (include/kvfp8.h);
+`prepare_decode` returns the prepared call so the two launches can also be enqueued
+one at a time.
 """
 
 from __future__ import annotations
@@ -53,6 +55,39 @@ def _index_tensor(x: t.Tensor) -> t.Tensor:
 
 
 def decode_attention_wrapper(q, paged_kv_cache, cache_batch_context=None):
+    call = prepare_decode(q, paged_kv_cache, cache_batch_context)
+    if call.args is not None:
+        call.run()
+    return call.output
+
+
+@dataclass
+class DecodeCall:
+    """One prepared decode call: its output tensor, its workspace and the C-ABI
+    argument tuple. `run()` enqueues both launches (`kvfp8_paged_decode`);
+    `split()` and `reduce()` enqueue them one at a time (`kvfp8_paged_decode_split`
+    then `kvfp8_paged_decode_reduce`, reference split and reduction kernels,
+    `decode_attention.py:146-189`). `args` is None for an empty batch."""
+
+    output: t.Tensor
+    workspace: t.Tensor | None
+    args: tuple | None
+    keep: tuple = ()          # every tensor whose address is in `args`
+
+    def run(self) -> None:
+        _native.check(_native.lib().kvfp8_paged_decode(*self.args), "kvfp8_paged_decode")
+
+    def split(self) -> None:
+        _native.check(_native.lib().kvfp8_paged_decode_split(*self.args), "kvfp8_paged_decode_split")
+
+    def reduce(self) -> None:
+        _native.check(_native.lib().kvfp8_paged_decode_reduce(*self.args), "kvfp8_paged_decode_reduce")
+
+
+def prepare_decode(q, paged_kv_cache, cache_batch_context=None) -> DecodeCall:
+    """Validate the arguments of `decode_attention_wrapper` (same forms, same
+    asserts and errors), allocate its output and workspace, and return the
+    prepared call without launching anything."""
     if cache_batch_context is None:
         kv = paged_kv_cache                       # PagedKVRead form
         k_cache, v_cache = kv.k, kv.v
@@ -89,7 +124,7 @@ def decode_attention_wrapper(q, paged_kv_cache, cache_batch_context=None):
                                  what="decode_attention_wrapper")
     output = t.empty((b, hq, d), dtype=q.dtype, device=q.device)
     if b == 0:
-        return output
+        return DecodeCall(output, None, None)
 
     if q.dtype not in _Q_DTYPES:
         raise ValueError(f"decode_attention_wrapper: unsupported q dtype {q.dtype}")
@@ -107,7 +142,7 @@ def decode_attention_wrapper(q, paged_kv_cache, cache_batch_context=None):
     ws_bytes = lib.kvfp8_decode_workspace_bytes(b, hq, hkv, d, block_table.shape[1], block_size, kv_code)
     workspace = t.empty(max(ws_bytes, 1), dtype=t.uint8, device=q.device)
 
-    rc = lib.kvfp8_paged_decode(
+    args = (
         q.data_ptr(), _native.dtype_code(q.dtype), q.stride(0), q.stride(1),
         b, hq, hkv, d,
         k_cache.data_ptr(), v_cache.data_ptr(), kv_code,
@@ -120,5 +155,5 @@ def decode_attention_wrapper(q, paged_kv_cache, cache_batch_context=None):
         output.data_ptr(), workspace.data_ptr(), workspace.numel(),
         _native.stream_handle(device),
     )
-    _native.check(rc, "kvfp8_paged_decode")
-    return output
+    keep = (q, k_cache, v_cache, k_scales, v_scales, block_table, cache_slots, context_lengths)
+    return DecodeCall(output, workspace, args, keep)

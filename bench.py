@@ -18,6 +18,7 @@ Prints one JSON line on stdout; progress goes to stderr.
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import math
 import os
@@ -32,6 +33,7 @@ sys.path.insert(0, str(ROOT))
 METRIC = "FP8 paged decode-attn HBM GB/s (% of peak) + KV tokens/s, B=32 4k ctx"
 PEAK_HBM_GBS = 8000.0
 MALL_BYTES = 256 * 2 ** 20
+MAX_POOLS = 64
 
 
 def log(*args):
@@ -71,7 +73,9 @@ class Setup:
                                                             s.head_dim, s.block_size)
         self.append_bytes = oracle.append_algorithmic_bytes(s.batch, s.num_kv_heads, s.head_dim, in_bytes=2)
         pool_bytes = self.w.num_blocks * s.block_size * s.num_kv_heads * (2 * s.head_dim + 8)
-        self.num_pools = max(2, math.ceil(2 * MALL_BYTES / pool_bytes) + 1)
+        # Enough pools to exceed twice the Infinity Cache; a tiny (launch-bound)
+        # workload such as cfg1 is capped at MAX_POOLS and stays cache-resident.
+        self.num_pools = min(MAX_POOLS, max(2, math.ceil(2 * MALL_BYTES / pool_bytes) + 1))
         self.pool_bytes = pool_bytes
         self.caches = []
         for _ in range(self.num_pools):
@@ -104,15 +108,31 @@ class Setup:
         return graphs
 
 
+class _NoGC:
+    """Python's cyclic garbage collector off inside a timed region (a collection
+    pause would leave the GPU idle between launches)."""
+
+    def __enter__(self):
+        gc.collect()
+        gc.disable()
+
+    def __exit__(self, *exc):
+        gc.enable()
+
+
 def time_steps(setup: Setup, steps: int, warmup: int):
-    """Two timed regions of `steps` steps each, after `warmup` eager steps:
-      * graph replay of the step (no host work between steps): ms per step;
-      * eager steps with HIP events around every decode-kernel launch on its
-        stream: mean kernel ms, and the eager ms per step.
+    """Three timed regions of `steps` calls each, after `warmup` eager steps:
+      * graph replay of the whole step (no host work between steps): ms per step;
+      * the split (decode) kernel alone, `steps` launches back to back on the
+        current stream between two HIP events, pools rotating: its mean launch
+        duration, the figure the roofline divides by;
+      * eager steps with HIP events on the dispatch packet of every decode-kernel
+        launch (hipExtLaunchKernel): per-dispatch kernel ms, and eager ms per step.
     """
     import ctypes
     import torch as t
     from aiproj_amd import _native
+    from aiproj_amd.kernals.decode_attention import prepare_decode
 
     lib = _native.lib()
     for i in range(warmup):
@@ -123,27 +143,43 @@ def time_steps(setup: Setup, steps: int, warmup: int):
         g.replay()
     t.cuda.synchronize()
     start, end = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
-    start.record()
-    for i in range(steps):
-        graphs[i % len(graphs)].replay()
-    end.record()
-    t.cuda.synchronize()
+    with _NoGC():
+        start.record()
+        for i in range(steps):
+            graphs[i % len(graphs)].replay()
+        end.record()
+        t.cuda.synchronize()
     graph_ms = start.elapsed_time(end) / steps
     del graphs
 
+    calls = [prepare_decode(setup.w.q, cache, setup.context) for cache in setup.caches]
+    for c in calls:
+        c.split()
+    t.cuda.synchronize()
+    with _NoGC():
+        start.record()
+        for i in range(steps):
+            calls[i % len(calls)].split()
+        end.record()
+        t.cuda.synchronize()
+    split_ms = start.elapsed_time(end) / steps
+    del calls
+
     _native.check(lib.kvfp8_timing_enable(steps), "kvfp8_timing_enable")
     t.cuda.synchronize()
-    start.record()
-    for i in range(steps):
-        setup.step(warmup + i)
-    end.record()
-    t.cuda.synchronize()
+    with _NoGC():
+        start.record()
+        for i in range(steps):
+            setup.step(warmup + i)
+        end.record()
+        t.cuda.synchronize()
     eager_ms = start.elapsed_time(end) / steps
     total_ms = ctypes.c_double(0.0)
     launches = ctypes.c_int64(0)
     _native.check(lib.kvfp8_timing_read(ctypes.byref(total_ms), ctypes.byref(launches)), "kvfp8_timing_read")
-    kernel_ms = total_ms.value / max(1, launches.value)
-    return graph_ms, eager_ms, kernel_ms, launches.value
+    dispatch_ms = total_ms.value / max(1, launches.value)
+    return {"graph_ms": graph_ms, "eager_ms": eager_ms, "split_ms": split_ms, "dispatch_ms": dispatch_ms,
+            "dispatch_launches": launches.value}
 
 
 def prefill_write(steps: int):
@@ -171,12 +207,13 @@ def prefill_write(steps: int):
         cache.append_kv(blocks, offsets, k, v)
     t.cuda.synchronize()
     start, end = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
-    start.record()
-    for i in range(steps):
-        cache, k, v = pools[i % 3]
-        cache.append_kv(blocks, offsets, k, v)
-    end.record()
-    t.cuda.synchronize()
+    with _NoGC():
+        start.record()
+        for i in range(steps):
+            cache, k, v = pools[i % 3]
+            cache.append_kv(blocks, offsets, k, v)
+        end.record()
+        t.cuda.synchronize()
     us = start.elapsed_time(end) / steps * 1e3
     nbytes = oracle.append_algorithmic_bytes(tokens, heads, dim, in_bytes=2)
     gbs = nbytes / (us * 1e-6) / 1e9
@@ -221,10 +258,11 @@ def model_decode(steps: int):
         t.cuda.synchronize()
         start, end = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
         timed = min(steps, new - 2)
-        start.record()
-        dec.generate(timed, use_graph=True)
-        end.record()
-        t.cuda.synchronize()
+        with _NoGC():
+            start.record()
+            dec.generate(timed, use_graph=True)
+            end.record()
+            t.cuda.synchronize()
     ms = start.elapsed_time(end) / timed
     kv_bytes = cfg.num_layers * batch * (prompt + 64) * cfg.num_kv_heads * (2 * cfg.head_dim + 8)
     weight_bytes = sum(p.numel() * p.element_size() for p in model.parameters())
@@ -337,14 +375,16 @@ def measure(name: str, steps: int, warmup: int):
     import torch as t
 
     setup = Setup(name, "cuda")
-    ms, eager_ms, kernel_ms, launches = time_steps(setup, steps, warmup)
+    times = time_steps(setup, steps, warmup)
+    ms, eager_ms, kernel_ms = times["graph_ms"], times["eager_ms"], times["split_ms"]
     s = setup.spec
     result = {
         "setup": setup,
         "ms_per_step": ms,
         "eager_ms_per_step": eager_ms,
         "split_kernel_ms": kernel_ms,
-        "timed_launches": launches,
+        "dispatch_kernel_ms": times["dispatch_ms"],
+        "dispatch_launches": times["dispatch_launches"],
         "step_bytes": setup.decode_bytes + setup.append_bytes,
         "gbs": (setup.decode_bytes + setup.append_bytes) / (ms * 1e-3) / 1e9,
         "kernel_gbs": setup.decode_bytes / (kernel_ms * 1e-3) / 1e9,
@@ -354,8 +394,9 @@ def measure(name: str, steps: int, warmup: int):
     }
     log(f"[{name}] B={s.batch} Hq={s.num_q_heads} Hkv={s.num_kv_heads} D={s.head_dim} tokens={s.total_tokens} "
         f"pools={setup.num_pools}x{setup.pool_bytes / 1e6:.0f}MB: {ms * 1e3:.1f} us/step (graph), "
-        f"{eager_ms * 1e3:.1f} us/step (eager), decode kernel {kernel_ms * 1e3:.1f} us "
-        f"({result['kernel_gbs']:.0f} GB/s), step {result['gbs']:.0f} GB/s")
+        f"{eager_ms * 1e3:.1f} us/step (eager), decode kernel {kernel_ms * 1e3:.1f} us back to back "
+        f"({result['kernel_gbs']:.0f} GB/s), {times['dispatch_ms'] * 1e3:.1f} us per-dispatch events, "
+        f"step {result['gbs']:.0f} GB/s")
     t.cuda.synchronize()
     return result
 
@@ -461,6 +502,9 @@ def main():
             "traffic": traffic_for("decode_mfma_kernel", s.name),
             "algorithmic_bytes_per_launch": main_result["setup"].decode_bytes,
             "mean_launch_us": round(main_result["split_kernel_ms"] * 1e3, 2),
+            "timing": (f"{args.steps} back-to-back launches of the decode kernel alone "
+                       "(kvfp8_paged_decode_split, pools rotating) between two HIP events on its stream"),
+            "dispatch_event_us": round(main_result["dispatch_kernel_ms"] * 1e3, 2),
         },
         "cpu_baseline": cpu,
         "secondary": secondary,

@@ -126,6 +126,47 @@ int kvfp8_paged_decode(const void* q_dev, int q_dtype, int64_t q_stride_b, int64
                        void* stream);
 
 /*
+ * The two launches of kvfp8_paged_decode as separate calls (same arguments; the
+ * same workspace must reach both, and nothing may write it in between):
+ *
+ * kvfp8_paged_decode_split enqueues the split kernel, reference
+ * `decode_attention_split_kernel` (src/torch_llm/kernals/decode_attention.py:194-434):
+ * it writes the output rows of the sequences it finishes whole and a partial
+ * softmax state (m, l, acc) per piece of every other sequence into the workspace.
+ *
+ * kvfp8_paged_decode_reduce enqueues the merge, reference
+ * `decode_attention_reduction_kernel` (decode_attention.py:437-550): out =
+ * sum_i 2^(m_i - M) acc_i / sum_i 2^(m_i - M) l_i over the pieces, zeros for empty
+ * sequences.
+ *
+ * Callers that combine pieces from elsewhere (a sequence split across devices) or
+ * time the split kernel alone use these; split followed by reduce on one stream
+ * equals kvfp8_paged_decode bit for bit.
+ */
+int kvfp8_paged_decode_split(const void* q_dev, int q_dtype, int64_t q_stride_b, int64_t q_stride_h,
+                             int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                             const void* k_cache_dev, const void* v_cache_dev, int kv_dtype,
+                             const float* k_scales_dev, const float* v_scales_dev,
+                             int64_t num_blocks, int32_t block_size,
+                             const int32_t* block_table_dev, int64_t bt_rows, int64_t bt_width,
+                             const void* slots_dev, int slots_dtype,
+                             const void* context_lengths_dev, int ctx_dtype,
+                             float sm_scale, void* out_dev,
+                             void* workspace_dev, int64_t workspace_bytes,
+                             void* stream);
+int kvfp8_paged_decode_reduce(const void* q_dev, int q_dtype, int64_t q_stride_b, int64_t q_stride_h,
+                              int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                              const void* k_cache_dev, const void* v_cache_dev, int kv_dtype,
+                              const float* k_scales_dev, const float* v_scales_dev,
+                              int64_t num_blocks, int32_t block_size,
+                              const int32_t* block_table_dev, int64_t bt_rows, int64_t bt_width,
+                              const void* slots_dev, int slots_dtype,
+                              const void* context_lengths_dev, int ctx_dtype,
+                              float sm_scale, void* out_dev,
+                              void* workspace_dev, int64_t workspace_bytes,
+                              void* stream);
+
+/*
  * RMSNorm forward over rows of x [rows, d_model] (row stride x_stride elements):
  *   inv_rms[r] = 1 / sqrt(mean_d x[r,d]^2 + eps); out[r,d] = (x[r,d] * inv_rms[r]) * weight[d]
  * in float32, out stored in x's dtype (f32/f16/bf16); weight f32/f16/bf16; inv_rms

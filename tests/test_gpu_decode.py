@@ -359,3 +359,26 @@ def test_back_to_back_calls_read_fresh_partial_states():
         expected = oracle_decode(q, cache, manager.block_table, context.cache_slots, lengths)
         t.testing.assert_close(out.double().cpu(), t.from_numpy(expected),
                                rtol=OUTPUT_TOLERANCE[t.bfloat16], atol=OUTPUT_TOLERANCE[t.bfloat16])
+
+
+@t.inference_mode()
+@pytest.mark.parametrize("cache_dtype,head_dim", [(FP8, 128), (FP8, 64), (t.bfloat16, 128), (t.float16, 80)])
+def test_split_then_reduce_equals_one_call(cache_dtype, head_dim):
+    # kvfp8_paged_decode_split followed by kvfp8_paged_decode_reduce on the same
+    # workspace gives the bits of kvfp8_paged_decode (MFMA and generic kernels);
+    # sequences the split kernel finishes whole are final before the reduce.
+    from aiproj_amd.kernals.decode_attention import prepare_decode
+
+    lengths = [3000, 17, 0, 1000, 1]
+    cache = PagedKVCache(sum(-(-n // 16) for n in lengths) + 8, 16, 8, head_dim, "cuda", cache_dtype)
+    nonzero = [max(n, 1) for n in lengths]
+    manager, context, _, _ = fill_decode_batch([cache], nonzero, 8, head_dim, 16, t.bfloat16, seed=15)
+    context.context_lengths.copy_(t.tensor(lengths, dtype=context.context_lengths.dtype))
+    q = t.randn(len(lengths), 32, head_dim, device="cuda", dtype=t.bfloat16)
+    whole = decode_attention_wrapper(q, cache, context)
+    call = prepare_decode(q, cache, context)
+    call.output.fill_(float("nan"))
+    call.split()
+    call.reduce()
+    assert t.equal(call.output, whole)
+    assert t.equal(whole[2], t.zeros_like(whole[2]))
