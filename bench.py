@@ -32,6 +32,7 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "FP8 paged decode-attn HBM GB/s (% of peak) + KV tokens/s, B=32 4k ctx"
 PEAK_HBM_GBS = 8000.0
+PEAK_BF16_TFLOPS = 2500.0     # dense bf16 MFMA
 MALL_BYTES = 256 * 2 ** 20
 MAX_POOLS = 64
 
@@ -45,11 +46,12 @@ def parse_args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
-    p.add_argument("--workload", default="north", choices=["north", "cfg2", "cfg3", "cfg4", "cfg1", "cfg5"],
-                   help="cfg5 runs only the decoder-LM leg and prints its own JSON line")
+    p.add_argument("--workload", default="north", choices=["north", "cfg2", "cfg3", "cfg4", "cfg1", "cfg5", "prefill"],
+                   help="cfg5 runs only the decoder-LM leg, prefill only the two prefill legs; "
+                        "each prints its own JSON line")
     p.add_argument("--secondary", default="cfg2", help="second workload to report ('' for none)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    p.add_argument("--no-prefill", action="store_true", help="skip the prefill-size append leg")
+    p.add_argument("--no-prefill", action="store_true", help="skip the prefill-size append and attention legs")
     p.add_argument("--no-model", action="store_true", help="skip the cfg5 model decode leg")
     p.add_argument("--no-others", action="store_true", help="skip the cfg1/cfg3/cfg4 decode legs")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
@@ -186,7 +188,8 @@ def prefill_write(steps: int):
     """Bulk quantized append at the cfg5 prefill size: every layer writes
     T = 64 sequences x 1024 prompt tokens = 65,536 tokens of 4 KV heads, D = 128,
     bf16 input, to shuffled slots (reference call site `model/attention.py:111-116`).
-    Three rotating pools; mean of `steps` back-to-back calls between two events."""
+    Three rotating pools, their writes captured in one HIP graph; mean over
+    `steps // 3` replays between two events."""
     import torch as t
     import oracle
     from aiproj_amd.inference.paged_kv_cache import PagedKVCache
@@ -206,15 +209,24 @@ def prefill_write(steps: int):
         cache, k, v = pools[i % 3]
         cache.append_kv(blocks, offsets, k, v)
     t.cuda.synchronize()
+    # One graph holds the three pools' writes, so the timed launches follow each
+    # other with no host time between them (a 40 us kernel is near Python's call cost).
+    graph = t.cuda.CUDAGraph()
+    with t.cuda.graph(graph):
+        for cache, k, v in pools:
+            cache.append_kv(blocks, offsets, k, v)
+    graph.replay()
+    t.cuda.synchronize()
+    reps = max(1, steps // 3)
     start, end = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
     with _NoGC():
         start.record()
-        for i in range(steps):
-            cache, k, v = pools[i % 3]
-            cache.append_kv(blocks, offsets, k, v)
+        for _ in range(reps):
+            graph.replay()
         end.record()
         t.cuda.synchronize()
-    us = start.elapsed_time(end) / steps * 1e3
+    us = start.elapsed_time(end) / (3 * reps) * 1e3
+    del graph
     nbytes = oracle.append_algorithmic_bytes(tokens, heads, dim, in_bytes=2)
     gbs = nbytes / (us * 1e-6) / 1e9
     del pools
@@ -230,6 +242,59 @@ def prefill_write(steps: int):
         "unit": "GB/s",
         "frac": round(gbs / PEAK_HBM_GBS, 4),
         "tokens_per_s": round(tokens / (us * 1e-6)),
+    }
+
+
+def prefill_attention(steps: int):
+    """Varlen causal prefill attention at the cfg5 prefill size: 64 packed prompts of
+    1024 tokens, 16 q / 4 KV heads, D = 128, bf16 (reference call site
+    `model/attention.py:101-110`, kernel `kernals/flash_attention.py:51-211`). Three
+    input sets rotate; `steps` back-to-back launches between two events. Roofline:
+    matrix cores, algorithmic flops 4 D Hq sum_b L_b (L_b + 1) / 2 (QK^T and PV over
+    the causal triangle)."""
+    import torch as t
+    from aiproj_amd.kernals.flash_attention import flash_attention_forward
+
+    batch, length, hq, hkv, d = 64, 1024, 16, 4, 128
+    total = batch * length
+    gen = t.Generator(device="cuda").manual_seed(7)
+    cu = t.arange(0, total + 1, length, device="cuda", dtype=t.int32)
+    sets = []
+    for _ in range(3):
+        q = t.randn(total, hq, d, device="cuda", dtype=t.bfloat16, generator=gen)
+        k = t.randn(total, hkv, d, device="cuda", dtype=t.bfloat16, generator=gen)
+        v = t.randn(total, hkv, d, device="cuda", dtype=t.bfloat16, generator=gen)
+        sets.append((q, k, v))
+    scale = 1.0 / math.sqrt(d)
+    for i in range(3):
+        flash_attention_forward(*sets[i], cu, length, scale)
+    t.cuda.synchronize()
+    start, end = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+    with _NoGC():
+        start.record()
+        for i in range(steps):
+            flash_attention_forward(*sets[i % 3], cu, length, scale)
+        end.record()
+        t.cuda.synchronize()
+    us = start.elapsed_time(end) / steps * 1e3
+    flops = 4 * d * hq * batch * length * (length + 1) // 2
+    tflops = flops / (us * 1e-6) / 1e12
+    del sets
+    t.cuda.empty_cache()
+    log(f"[prefill attention] {batch} x {length} tokens, {hq}q/{hkv}kv, D {d}, bf16: {us:.1f} us "
+        f"({tflops:.0f} TFLOP/s)")
+    return {
+        "workload": f"cfg5 prefill attention: {batch} packed causal prompts x {length} tokens, {hq}q/{hkv}kv heads, "
+                    f"D {d}, bf16",
+        "kernel": "prefill_fa_kernel",
+        "bound": "mfma",
+        "us_per_call": round(us, 2),
+        "algorithmic_flops_per_call": flops,
+        "achieved": round(tflops, 1),
+        "peak": PEAK_BF16_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+        "tokens_per_s": round(total / (us * 1e-6)),
     }
 
 
@@ -421,6 +486,10 @@ def main():
     if args.workload == "cfg5":
         print(json.dumps({"workload": "cfg5", "model_decode": model_decode(args.steps)}), flush=True)
         return
+    if args.workload == "prefill":
+        print(json.dumps({"workload": "prefill", "prefill_write": prefill_write(args.steps),
+                          "prefill_attention": prefill_attention(args.steps)}), flush=True)
+        return
 
     copy_gbs = copy_bandwidth_gbs()
     log(f"device copy bandwidth: {copy_gbs:.0f} GB/s")
@@ -464,6 +533,7 @@ def main():
             }
             del r
     prefill = None if args.no_prefill else prefill_write(max(10, args.steps // 2))
+    prefill_attn = None if args.no_prefill else prefill_attention(max(10, args.steps // 2))
     model = None if args.no_model else model_decode(100)
     kernel_gbs = main_result["kernel_gbs"]
     line = {
@@ -510,6 +580,7 @@ def main():
         "secondary": secondary,
         "other_workloads": others,
         "prefill_write": prefill,
+        "prefill_attention": prefill_attn,
         "model_decode": model,
     }
     print(json.dumps(line), flush=True)
