@@ -174,6 +174,66 @@ rmsnorm_kernel(NormArgs a, int vec_ok) {
     }
 }
 
+// One workgroup per row (grid-strided over the rows) for aligned rows of up to
+// 256 x 8 x VPT elements: thread t owns the 16-byte vectors t, t + 256, ... of the
+// row in every tensor, so the row is read once, with 256 independent loads in
+// flight per tensor. The sum of squares is reduced across the wave (shuffles)
+// and then across the four waves through LDS, with one barrier per row (the LDS
+// slot alternates by row parity, so a fast wave writing row r + 2 cannot overwrite
+// values a slow wave still reads for row r: the barrier of row r + 1 lies between).
+// A decode step's 64 rows then run as 64 workgroups instead of 64 waves.
+template <int DT, int WT, bool kFused, int VPT>
+__global__ void __launch_bounds__(kNormThreads)
+rmsnorm_row_kernel(NormArgs a) {
+    using T = typename Elem<DT>::T;
+    using W = typename Elem<WT>::T;
+    __shared__ float partial[2][kNormThreads / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int D = a.d_model;
+    float w[VPT][kNormVec];
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+        const int d0 = (tid + kNormThreads * k) * kNormVec;
+        load8<WT>(reinterpret_cast<const W*>(a.weight) + d0, true, d0 < D ? kNormVec : 0, w[k]);
+    }
+    int parity = 0;
+    for (int64_t r = blockIdx.x; r < a.rows; r += gridDim.x, parity ^= 1) {
+        float v[VPT][kNormVec];
+        float ss = 0.0f;
+#pragma unroll
+        for (int k = 0; k < VPT; ++k) {
+            const int d0 = (tid + kNormThreads * k) * kNormVec;
+            if (d0 < D) {
+                row_chunk<DT, kFused>(a, r, d0, kNormVec, true, v[k]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < kNormVec; ++i) v[k][i] = 0.0f;
+            }
+#pragma unroll
+            for (int i = 0; i < kNormVec; ++i) ss += v[k][i] * v[k][i];
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+        if (lane == 0) partial[parity][wave] = ss;
+        __syncthreads();
+        float total = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kNormThreads / 64; ++i) total += partial[parity][i];
+        const float inv = 1.0f / sqrtf(total / (float)D + a.eps);
+        if (tid == 0 && a.inv_rms) a.inv_rms[r] = inv;
+#pragma unroll
+        for (int k = 0; k < VPT; ++k) {
+            const int d0 = (tid + kNormThreads * k) * kNormVec;
+            if (d0 >= D) continue;
+            if constexpr (kFused) store8<DT>(reinterpret_cast<T*>(a.state_out) + r * a.state_stride + d0, true, kNormVec, v[k]);
+            float o[kNormVec];
+#pragma unroll
+            for (int i = 0; i < kNormVec; ++i) o[i] = (v[k][i] * inv) * w[k][i];
+            store8<DT>(reinterpret_cast<T*>(a.out) + r * a.out_stride + d0, true, kNormVec, o);
+        }
+    }
+}
+
 }  // namespace kvfp8
 
 using namespace kvfp8;
@@ -194,6 +254,17 @@ hipError_t launch_norm(const NormArgs& a, hipStream_t s) {
     const bool vec = a.d_model % kNormVec == 0 && aligned(a.x, a.x_stride, es) && aligned(a.out, a.out_stride, es) &&
                      aligned(a.update, a.update_stride, es) && aligned(a.state_out, a.state_stride, es) &&
                      aligned(a.weight, 0, esize(WT));
+    // Aligned rows of up to 8192 elements: a workgroup per row (at most 4096
+    // workgroups in flight, each then loops over rows).
+    const int vectors = (a.d_model + kNormVec - 1) / kNormVec;
+    if (vec && vectors <= 4 * kNormThreads) {
+        const int vpt = (vectors + kNormThreads - 1) / kNormThreads;
+        const dim3 grid((unsigned)(a.rows < 4096 ? a.rows : 4096)), block(kNormThreads);
+        if (vpt == 1) hipLaunchKernelGGL((rmsnorm_row_kernel<DT, WT, F, 1>), grid, block, 0, s, a);
+        else if (vpt == 2) hipLaunchKernelGGL((rmsnorm_row_kernel<DT, WT, F, 2>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((rmsnorm_row_kernel<DT, WT, F, 4>), grid, block, 0, s, a);
+        return hipGetLastError();
+    }
     int64_t blocks = (a.rows + 3) / 4;
     blocks = blocks < 1 ? 1 : (blocks > 65536 ? 65536 : blocks);
     hipLaunchKernelGGL((rmsnorm_kernel<DT, WT, F>), dim3((unsigned)blocks), dim3(kNormThreads), 0, s, a, (int)vec);
