@@ -601,10 +601,14 @@ decode_mfma_kernel(MfmaArgs a) {
     // behind its partner, so both finish together.
     const int partner = (wave ^ 4) < waves ? (wave ^ 4) : wave;
     int32_t steps_done = 0;
+    // The counters are relaxed workgroup-scope atomics on the LDS array (ds_write /
+    // ds_read); a volatile access through a generic pointer would compile to flat
+    // system-coherent memory operations followed by a full vmcnt/lgkmcnt wait.
     auto keep_pace = [&]() {
         ++steps_done;
-        if (lane == 0) *(volatile int32_t*)&progress[wave] = steps_done;
-        const int32_t other = uniform(*(volatile int32_t*)&progress[partner]);
+        if (lane == 0) __hip_atomic_store(&progress[wave], steps_done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        const int32_t other =
+            uniform(__hip_atomic_load(&progress[partner], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
         if (steps_done < other) __builtin_amdgcn_s_setprio(2);
         else __builtin_amdgcn_s_setprio(0);
     };
