@@ -104,6 +104,41 @@ __device__ __forceinline__ uint32_t f16_bits(float x) {
     return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
 }
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Two floats -> one dword of two 16-bit values, rounded to nearest even (one
+// v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32).
+template <bool kF16>
+__device__ __forceinline__ uint32_t pack2(float x0, float x1) {
+    const f32x2_t v = {x0, x1};
+    if constexpr (kF16) return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2_t));
+    else return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+
+// Maximum over lanes l, l ^ 16, l ^ 32 and l ^ 48. Each permlane swap leaves the
+// values of a lane pair (l, l ^ 16), then (l, l ^ 32), in the two results, so
+// their maximum is the pair's in every lane; no LDS round trip.
+__device__ __forceinline__ float max_across_rows(float x) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, x);
+    const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    const float y = fmaxf(as_float(a[0]), as_float(a[1]));
+    const uint32_t v = __builtin_bit_cast(uint32_t, y);
+    const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return fmaxf(as_float(b[0]), as_float(b[1]));
+}
+
+// Sum over the same four lanes (equal in all four: float addition commutes).
+__device__ __forceinline__ float sum_across_rows(float x) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, x);
+    const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    const float y = as_float(a[0]) + as_float(a[1]);
+    const uint32_t v = __builtin_bit_cast(uint32_t, y);
+    const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return as_float(b[0]) + as_float(b[1]);
+}
+
 // Eight floats -> operand (bf16, or f16 for f16 inputs; split for float32).
 template <bool kF16, bool kSplit>
 __device__ __forceinline__ Opnd<kSplit> pack8(const float (&x)[8]) {
@@ -424,44 +459,124 @@ prefill_attention_kernel(PrefillArgs a) {
 // ---------------------------------------------------------------------------
 // Eight-wave kernel for 16-bit inputs with D in {64, 128}.
 //
-// A workgroup of eight waves takes one (sequence, KV head, query block): its
-// waves are `gw` q heads x (8 / gw) groups of 32 query rows, and its K/V blocks of
-// 64 keys are staged once in LDS for all of them. Every wave keeps its whole state
-// (Q^T operands, accumulators, scores) within 256 registers, so two waves share
-// each SIMD and one wave's softmax runs while the other's MFMAs do.
-// Work items run (sequence, KV head) by (sequence, KV head), longest query block
-// first, and each XCD takes one contiguous run of items, so the query blocks of
-// one sequence and head meet its K/V in the same L2.
+// An item is one (sequence, KV head, query block): the eight waves are `gw` q heads
+// x (8 / gw) groups of 32 query rows, and its K/V blocks of 64 keys are staged once
+// in LDS for all of them. Every wave keeps its whole state (Q^T operands,
+// accumulators, scores) within 256 registers, so two waves share each SIMD.
+// Workgroups are persistent, one per CU, and walk a list of items with the K/V
+// and Q loads of the next item issued during the current one. Each XCD takes one
+// contiguous run of (sequence, KV head) units, so the query blocks of one sequence
+// and head meet its K/V in the same L2; it orders them in groups of kGroupUnits
+// units, longest query block first across the group.
 // ---------------------------------------------------------------------------
 constexpr int kFaRows = 32;        // query rows per wave
 constexpr int kFaTiles = kFaRows / 16;
 constexpr int kFaWaves = 8;
 constexpr int kFaThreads = 64 * kFaWaves;
 constexpr int kXcds = 8;           // workgroups are dispatched round-robin over the XCDs
+constexpr int kGroupUnits = 8;     // units per longest-first group (their K/V: 8 x 512 KB at L 1024, D 128)
 constexpr int kFaBufs = 3;         // K/V block buffers in LDS
+
+// Wave-uniform loads through the scalar data cache, waited for at once. The
+// compiler would issue a vector load for a plain load of this memory (the kernel
+// also stores to global memory) and then wait for every vector-memory operation in
+// flight, K/V prefetches included.
+__device__ __forceinline__ int64_t uniform_load_i64(const int64_t* p) {
+    uint64_t v;
+    __asm__ volatile("s_load_dwordx2 %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p) : "memory");
+    return (int64_t)v;
+}
+__device__ __forceinline__ int32_t uniform_load_i32(const int32_t* p) {
+    uint32_t v;
+    __asm__ volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p) : "memory");
+    return (int32_t)v;
+}
+
+// One work item: query block qb of a unit (sequence b, KV head hk, head block hb).
+struct FaItem {
+    int32_t s0;        // first token of the sequence
+    int32_t L;         // its length, capped at max_seq_len
+    int32_t qb;
+    int32_t hk, hb;
+    int32_t n_kv;      // K/V blocks of 64 keys the query block reads
+};
+
+// The items of one workgroup. XCD x = blockIdx % 8 owns units [x upx, (x + 1) upx),
+// ordered in groups of kGroupUnits units, longest query block first across each
+// group: item t is query block qblocks - 1 - (t % span) / gsize of unit
+// g kGroupUnits + (t % span) % gsize, g = t / span. The XCD's P workgroups take
+// these items in snake order: in round k, workgroup c takes item k P + c (k even)
+// or k P + P - 1 - c (k odd), so long and short query blocks pair up.
+struct FaSchedule {
+    int32_t u_lo;      // first unit of the XCD
+    int32_t nu;        // its units
+    int32_t T;         // its items, nu * qblocks
+    int32_t P;         // workgroups per XCD
+    int32_t c;         // this workgroup's index within the XCD
+};
+
+// The first item at or after round k that has query rows (query blocks past the
+// end of a shorter sequence are skipped); k is left at its round. False when the
+// workgroup has no more items. (The host keeps items and tokens below 2^31.)
+__device__ __forceinline__ bool fa_item(const PrefillArgs& a, const FaSchedule& sc, int32_t& k, FaItem& it) {
+    const int32_t span = kGroupUnits * a.qblocks;
+    for (;; ++k) {
+        const int32_t t = k * sc.P + ((k & 1) ? sc.P - 1 - sc.c : sc.c);
+        if (t >= sc.T) return false;
+        const int32_t g = t / span, r = t - g * span;
+        const int32_t gsize = min(kGroupUnits, sc.nu - g * kGroupUnits);
+        const int32_t qbi = r / gsize;
+        const int32_t unit = sc.u_lo + g * kGroupUnits + (r - qbi * gsize);
+        const int32_t b = unit / (a.hkv * a.blocks_per_kv);
+        const int32_t rest = unit - b * a.hkv * a.blocks_per_kv;
+        int64_t s0, s1;
+        if (a.cu64) {
+            s0 = uniform_load_i64(reinterpret_cast<const int64_t*>(a.cu) + b);
+            s1 = uniform_load_i64(reinterpret_cast<const int64_t*>(a.cu) + b + 1);
+        } else {
+            s0 = uniform_load_i32(reinterpret_cast<const int32_t*>(a.cu) + b);
+            s1 = uniform_load_i32(reinterpret_cast<const int32_t*>(a.cu) + b + 1);
+        }
+        s0 = s0 < 0 ? 0 : s0;
+        s1 = s1 > a.total_tokens ? a.total_tokens : s1;
+        int64_t len64 = s1 > s0 ? s1 - s0 : 0;
+        len64 = len64 < a.max_len ? len64 : a.max_len;
+        const int L = (int)len64;
+        const int qb = a.qblocks - 1 - qbi;
+        const int r0 = qb * a.rows;
+        if (r0 >= L) continue;
+        it.s0 = (int32_t)s0;
+        it.L = L;
+        it.qb = qb;
+        it.hk = rest / a.blocks_per_kv;
+        it.hb = rest - it.hk * a.blocks_per_kv;
+        it.n_kv = (min(L, r0 + a.rows) + kKeys - 1) / kKeys;
+        return true;
+    }
+}
 
 template <int C, bool kF16>
 __global__ void __launch_bounds__(kFaThreads)
-prefill_fa_kernel(PrefillArgs a, int64_t items, int64_t per_xcd) {
+prefill_fa_kernel(PrefillArgs a, int32_t units, int32_t upx, int32_t per_xcd) {
     constexpr int kD = 64 * C;
     constexpr int ROW = kD * 2;                      // bytes per K/V row
     constexpr int CPR = kD * 2 / 16;                 // 16-byte chunks per row
     constexpr int CPT = kKeys * CPR / kFaThreads;    // chunks per thread per tensor and block
-    // s_waitcnt immediate for "vmcnt <= the 2 CPT loads of one block" (expcnt and
-    // lgkmcnt left at their maxima): older loads done, the newest block's in flight.
-    constexpr int kKeep = 2 * CPT;
-    constexpr int kVmcntKeep = (kKeep & 15) | (7 << 4) | (0 << 8) | (((kKeep >> 4) & 3) << 14);
+    constexpr int NB = 4 * C;                        // head dims per lane in the PV product
+    constexpr int KS = 2 * C;                        // 32-dim steps of the QK product
+    // Vector-memory instructions a wave issues: kBlockLoads per K/V block, kQLoads
+    // for its Q operands of one item.
+    constexpr int kBlockLoads = 2 * CPT;
+    constexpr int kQLoads = kFaTiles * KS;
     // Workgroup barrier that does not drain the K/V prefetch: __syncthreads() would
-    // wait for every outstanding load. This wave's LDS reads and its loads older
-    // than the newest block are complete (s_waitcnt above); the compiler-level fences
-    // keep every LDS access on its side of the barrier.
+    // wait for every outstanding load. Before it the wave waits (s_waitcnt) for its
+    // LDS reads and for its loads older than the ones it keeps in flight; the
+    // compiler-level fences keep every LDS access on its side of the barrier.
     auto barrier = [&]() {
         __asm__ volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         __asm__ volatile("" ::: "memory");
     };
-    constexpr int NB = 4 * C;                        // head dims per lane in the PV product
-    constexpr int KS = 2 * C;                        // 32-dim steps of the QK product
     // K/V blocks go from global memory straight into LDS (global_load_lds_dwordx4:
     // lane t of an instruction writes the t-th 16 bytes after the wave's base), so
     // the layout is the load order: chunk slot c holds row c / CPR, chunk
@@ -471,86 +586,94 @@ prefill_fa_kernel(PrefillArgs a, int64_t items, int64_t per_xcd) {
     __shared__ __attribute__((aligned(16))) uint8_t lds_v[kFaBufs][kKeys * ROW];
     typedef __attribute__((address_space(3))) void* lds_ptr;
 
-    // Item of this workgroup: XCD x = blockIdx % 8 takes items [x per_xcd, (x + 1) per_xcd).
-    const int64_t item = (int64_t)(blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
-    if (item >= items) return;
-    // Items: (sequence, KV head, head block) major, query block descending.
-    const int64_t unit = item / a.qblocks;
-    const int qb = a.qblocks - 1 - (int)(item - unit * a.qblocks);
-    const int b = (int)(unit / ((int64_t)a.hkv * a.blocks_per_kv));
-    const int64_t rest = unit - (int64_t)b * a.hkv * a.blocks_per_kv;
-    const int hk = (int)(rest / a.blocks_per_kv);
-    const int hb = (int)(rest - (int64_t)hk * a.blocks_per_kv);
+    // LDS byte addresses of the K and V buffers (the DMA loads take them in m0).
+    const uint32_t k_lds0 = (uint32_t)(uintptr_t)(lds_ptr)(&lds_k[0][0]);
+    const uint32_t v_lds0 = (uint32_t)(uintptr_t)(lds_ptr)(&lds_v[0][0]);
 
-    int64_t s0, s1;
-    if (a.cu64) {
-        s0 = reinterpret_cast<const int64_t*>(a.cu)[b];
-        s1 = reinterpret_cast<const int64_t*>(a.cu)[b + 1];
-    } else {
-        s0 = reinterpret_cast<const int32_t*>(a.cu)[b];
-        s1 = reinterpret_cast<const int32_t*>(a.cu)[b + 1];
-    }
-    s0 = s0 < 0 ? 0 : s0;
-    s1 = s1 > a.total_tokens ? a.total_tokens : s1;
-    int64_t len64 = s1 > s0 ? s1 - s0 : 0;
-    len64 = len64 < a.max_len ? len64 : a.max_len;
-    const int L = (int)len64;
-    const int r0 = qb * a.rows;
-    if (r0 >= L) return;                                  // whole workgroup
+    FaSchedule sc;
+    sc.P = per_xcd;
+    sc.c = (int32_t)(blockIdx.x / kXcds);
+    sc.u_lo = (int32_t)(blockIdx.x % kXcds) * upx;
+    sc.nu = max(min(units, sc.u_lo + upx) - sc.u_lo, 0);
+    sc.T = sc.nu * a.qblocks;
+
+    // Two cursors walk the workgroup's items block by block: the load cursor
+    // (lk, li, lkb) two K/V blocks ahead of the compute cursor (ck, ci, ckb).
+    int32_t lk = 0;
+    FaItem li;
+    bool lhas = fa_item(a, sc, lk, li);
+    if (!lhas) return;                                   // whole workgroup: no items
+    int lkb = 0;
+    int32_t ck = lk;
+    FaItem ci = li;
+    int ckb = 0;
 
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int m16 = lane & 15, j = lane >> 4;
     const int G = a.hq / a.hkv;
     const int gw = a.heads_per_block;
-    const int hq = hk * G + hb * gw + wave % gw;
-    const int qa = r0 + kFaRows * (wave / gw);            // first query row of this wave
-    const bool active = qa < L;
-    const int kv_end = min(L, r0 + a.rows);               // keys the workgroup needs
-    const int n_kv = (kv_end + kKeys - 1) / kKeys;
-    const int wave_nkv = active ? (min(L, qa + kFaRows) + kKeys - 1) / kKeys : 0;
     const int64_t q_row = (int64_t)a.hq * kD * 2;         // bytes between tokens
     const int64_t kv_row = (int64_t)a.hkv * kD * 2;
 
-    // Q^T operands: lane (row 16 qt + l % 16, l / 16) holds dims 32 s + 8 (l / 16) .. + 7.
-    u32x4_t qop[kFaTiles][KS];
-#pragma unroll
-    for (int qt = 0; qt < kFaTiles; ++qt) {
-        const int row = qa + 16 * qt + m16;
-        const bool rv = active && row < L;
-#pragma unroll
-        for (int s = 0; s < KS; ++s) {
-            const uint8_t* p = rv ? a.q + (s0 + row) * q_row + ((int64_t)hq * kD + 32 * s + 8 * j) * 2 : a.q;
-            const u32x4_t x = *reinterpret_cast<const u32x4_t*>(p);
-            qop[qt][s] = rv ? x : u32x4_t{0u, 0u, 0u, 0u};
-        }
-    }
-
-    // Asynchronous K/V block load into LDS buffer `buf`. Keys past the sequence read
-    // its last key (finite data, masked out of the scores).
+    // Asynchronous load of block kb of item it into LDS buffer `buf`. Keys past the
+    // sequence read its last key (finite data, masked out of the scores).
     //
     // The loads are issued as inline assembly: the compiler's wait insertion would
     // otherwise assume that any LDS read may alias an LDS write in flight and wait
     // for every outstanding load before it (defeating the prefetch). The kernel
     // waits for them itself: the s_waitcnt before each block's closing barrier.
-    auto load_block = [&](int kb, int buf) {
+    auto load_block = [&](const FaItem& it, int kb, int buf) {
 #pragma unroll
         for (int i = 0; i < CPT; ++i) {
             const int c = threadIdx.x + kFaThreads * i;         // slot written by this lane
             const int row = c / CPR;
             const int chunk = (c % CPR) ^ (row % CPR);
-            const int key = min(kb * kKeys + row, L - 1);
-            const int64_t off = (s0 + key) * kv_row + (int64_t)hk * kD * 2 + 16 * chunk;
-            const int wave_slot = kFaThreads * i + 64 * wave;   // first slot of this wave's instruction
-            const uint32_t k_lds = (uint32_t)(uintptr_t)(lds_ptr)(&lds_k[buf][16 * wave_slot]);
-            const uint32_t v_lds = (uint32_t)(uintptr_t)(lds_ptr)(&lds_v[buf][16 * wave_slot]);
+            const int key = min(kb * kKeys + row, it.L - 1);
+            const int64_t off = (int64_t)(it.s0 + key) * kv_row + (int64_t)it.hk * kD * 2 + 16 * chunk;
+            // First slot of this wave's instruction (wave-uniform).
+            const uint32_t slot = (uint32_t)buf * (kKeys * ROW) + 16u * (uint32_t)(kFaThreads * i + 64 * wave);
             const uint8_t* kg = a.k + off;
             const uint8_t* vg = a.v + off;
             __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
-                             :: "s"(__builtin_amdgcn_readfirstlane(k_lds)), "v"(kg) : "memory");
+                             :: "s"(__builtin_amdgcn_readfirstlane(k_lds0 + slot)), "v"(kg) : "memory");
             __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
-                             :: "s"(__builtin_amdgcn_readfirstlane(v_lds)), "v"(vg) : "memory");
+                             :: "s"(__builtin_amdgcn_readfirstlane(v_lds0 + slot)), "v"(vg) : "memory");
         }
     };
+    // Load the load cursor's block into `buf` and advance the cursor; false when
+    // every block has been loaded. Every wave issues the same loads.
+    auto load_next = [&](int buf) -> bool {
+        if (!lhas) return false;
+        load_block(li, lkb, buf);
+        if (++lkb == li.n_kv) {
+            ++lk;
+            lhas = fa_item(a, sc, lk, li);
+            lkb = 0;
+        }
+        return true;
+    };
+
+    // This wave's rows of an item: q head hq, query rows qa .. qa + 31.
+    auto wave_head = [&](const FaItem& it) { return it.hk * G + it.hb * gw + wave % gw; };
+    auto wave_row = [&](const FaItem& it) { return it.qb * a.rows + kFaRows * (wave / gw); };
+
+    // Q^T operands: lane (row 16 qt + l % 16, l / 16) holds dims 32 s + 8 (l / 16) .. + 7.
+    // Rows past the sequence load its last row: their results are never stored, and
+    // every row's softmax is its own, so they need no zeroing (which would have to
+    // wait for the loads where they are issued).
+    u32x4_t qop[kFaTiles][KS];
+    auto load_q = [&](const FaItem& it) {
+        const int hq_n = wave_head(it), qa_n = wave_row(it);
+#pragma unroll
+        for (int qt = 0; qt < kFaTiles; ++qt) {
+            const int row = min(qa_n + 16 * qt + m16, it.L - 1);
+#pragma unroll
+            for (int s = 0; s < KS; ++s)
+                qop[qt][s] = *reinterpret_cast<const u32x4_t*>(a.q + (int64_t)(it.s0 + row) * q_row +
+                                                               ((int64_t)hq_n * kD + 32 * s + 8 * j) * 2);
+        }
+    };
+
     // Per-lane byte offsets of the operand reads (key tile bases are multiples of 16
     // rows, which the swizzle ignores: (16 t + r) % CPR = r % CPR):
     //   K operand, 32-dim step s: row m16, chunk 4 s + j;
@@ -564,27 +687,38 @@ prefill_fa_kernel(PrefillArgs a, int64_t items, int64_t per_xcd) {
         v_off[e] = r * ROW + 16 * (((NB * m16) >> 3) ^ (r % CPR)) + ((NB * m16 * 2) & 15);
     }
 
+    // Compute state of the current item: accumulators o[qt][nb] for the head dims;
+    // l[qt] holds a lane's part (16 of every 64 keys) of its row's float32
+    // probability sum.
     f32x4_t o[kFaTiles][NB];
+    float m[kFaTiles], neg_m[kFaTiles], l[kFaTiles];
+    int hq = 0, qa = 0, wave_nkv = 0;
+    bool active = false;
+    auto enter = [&](const FaItem& it) {
+        hq = wave_head(it);
+        qa = wave_row(it);
+        active = qa < it.L;
+        wave_nkv = active ? (min(it.L, qa + kFaRows) + kKeys - 1) / kKeys : 0;
 #pragma unroll
-    for (int qt = 0; qt < kFaTiles; ++qt)
+        for (int qt = 0; qt < kFaTiles; ++qt) {
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) o[qt][nb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    float m[kFaTiles], l[kFaTiles];
-#pragma unroll
-    for (int qt = 0; qt < kFaTiles; ++qt) {
-        m[qt] = kNegInf;
-        l[qt] = 0.0f;
-    }
+            for (int nb = 0; nb < NB; ++nb) o[qt][nb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            m[qt] = kNegInf;
+            neg_m[qt] = 0.0f;
+            l[qt] = 0.0f;
+        }
+    };
 
-    // The buffer index is a compile-time constant in every call (the block loop is
-    // unrolled by kFaBufs), so all LDS operand addresses are a per-lane offset plus
-    // an immediate.
-    auto compute_block = [&](int kb, auto buf_c) {
+    // A block's work is three phases: qk (S^T = K Q^T, matrix cores), softmax
+    // (vector ALU) and pv (O^T += V^T P^T, matrix cores). The buffer index is a
+    // compile-time constant in every call (the block loop is unrolled by kFaBufs),
+    // so all LDS operand addresses are a per-lane offset plus an immediate.
+    f32x4_t sacc[4][kFaTiles];
+    u32x4_t pop[kFaTiles][2];           // P^T operands; pp holds keys 16 (2 pp + i / 4) + 4 j + i % 4
+    auto qk = [&](auto buf_c) {
         constexpr int buf = decltype(buf_c)::value;
         const uint8_t* kl = lds_k[buf];
-        const uint8_t* vl = lds_v[buf];
-        // S^T tiles: 4 key tiles x 2 row tiles; each K operand feeds both row tiles.
-        f32x4_t sacc[4][kFaTiles];
+        // 4 key tiles x 2 row tiles; each K operand feeds both row tiles.
 #pragma unroll
         for (int s = 0; s < KS; ++s) {
 #pragma unroll
@@ -595,35 +729,30 @@ prefill_fa_kernel(PrefillArgs a, int64_t items, int64_t per_xcd) {
                     sacc[kt][qt] = mma16<kF16>(kop, qop[qt][s], s == 0 ? f32x4_t{0.0f, 0.0f, 0.0f, 0.0f} : sacc[kt][qt]);
             }
         }
+    };
+    auto softmax = [&](int kb, int L) {
         const bool full = kb * kKeys + kKeys - 1 <= qa && kb * kKeys + kKeys <= L;   // wave-uniform
-        // Online softmax per row tile; P^T operand pp holds keys 16 (2 pp + i / 4) + 4 j + i % 4.
-        u32x4_t pop[kFaTiles][2];
 #pragma unroll
         for (int qt = 0; qt < kFaTiles; ++qt) {
             // Raw scores (the scale is applied inside the exponent below).
-            float sc[16];
+            float sc_[16];
 #pragma unroll
             for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-                for (int jj = 0; jj < 4; ++jj) sc[4 * kt + jj] = sacc[kt][qt][jj];
+                for (int jj = 0; jj < 4; ++jj) sc_[4 * kt + jj] = sacc[kt][qt][jj];
             if (!full) {
-                const int row = qa + 16 * qt + m16;
+                // Keep key kb * 64 + 16 kt + 4 j + jj when it is <= min(row, L - 1).
+                const int lim = min(qa + 16 * qt + m16, L - 1) - (kb * kKeys + 4 * j);
 #pragma unroll
-                for (int kt = 0; kt < 4; ++kt) {
+                for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-                    for (int jj = 0; jj < 4; ++jj) {
-                        const int key = kb * kKeys + 16 * kt + 4 * j + jj;
-                        const bool keep = (key <= row) & (key < L);
-                        sc[4 * kt + jj] = keep ? sc[4 * kt + jj] : kNegInf;
-                    }
-                }
+                    for (int jj = 0; jj < 4; ++jj)
+                        sc_[4 * kt + jj] = 16 * kt + jj <= lim ? sc_[4 * kt + jj] : kNegInf;
             }
-            float mx = sc[0];
+            float mx = sc_[0];
 #pragma unroll
-            for (int i = 1; i < 16; ++i) mx = fmaxf(mx, sc[i]);
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            mx *= a.scale_log2;                       // base-2 units (scale > 0 keeps the order)
+            for (int i = 1; i < 16; ++i) mx = fmaxf(mx, sc_[i]);
+            mx = max_across_rows(mx) * a.scale_log2;   // base-2 units (scale > 0 keeps the order)
             // Lazy rescale: the accumulators keep a reference max m that is only moved
             // when some row's max grows by more than 2^8 (p <= 256 meanwhile, far
             // inside float32 and bf16 range), so the accumulators are rarely scaled.
@@ -635,25 +764,25 @@ prefill_fa_kernel(PrefillArgs a, int64_t items, int64_t per_xcd) {
 #pragma unroll
                 for (int nb = 0; nb < NB; ++nb) o[qt][nb] *= alpha;
                 m[qt] = m_new;
+                neg_m[qt] = -m_use;
             }
-            const float neg_m = m[qt] == kNegInf ? 0.0f : -m[qt];
             float pr[16];
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                pr[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[i], a.scale_log2, neg_m));
+                pr[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc_[i], a.scale_log2, neg_m[qt]));
                 l[qt] += pr[i];
             }
 #pragma unroll
-            for (int pp = 0; pp < 2; ++pp) {
-                float x[8];
+            for (int pp = 0; pp < 2; ++pp)
 #pragma unroll
-                for (int i = 0; i < 8; ++i) x[i] = pr[8 * pp + i];
-                pop[qt][pp] = pack8<kF16, false>(x).h;
-            }
+                for (int w = 0; w < 4; ++w) pop[qt][pp][w] = pack2<kF16>(pr[8 * pp + 2 * w], pr[8 * pp + 2 * w + 1]);
         }
-        // O^T += V^T P^T: the lane reads NB dims at NB (l % 16) of the eight V rows of
-        // its keys; row pairs are transposed into one operand per dim, which feeds
-        // both row tiles.
+    };
+    // The lane reads NB dims at NB (l % 16) of the eight V rows of its keys; row
+    // pairs are transposed into one operand per dim, which feeds both row tiles.
+    auto pv = [&](auto buf_c) {
+        constexpr int buf = decltype(buf_c)::value;
+        const uint8_t* vl = lds_v[buf];
 #pragma unroll
         for (int pp = 0; pp < 2; ++pp) {
             constexpr int VW = NB / 2;       // dwords per row and lane
@@ -683,58 +812,110 @@ prefill_fa_kernel(PrefillArgs a, int64_t items, int64_t per_xcd) {
             }
         }
     };
-
-    // Three LDS buffers: block kb + 2 streams in while block kb is computed. Before
-    // the barrier that ends block kb every wave waits for its loads of block kb + 1
-    // (issued a block earlier); the barrier then publishes them, and it also ends
-    // the last reads of the buffer that block kb + 3 will overwrite.
-    auto step = [&](int kb, auto buf_c) {
-        constexpr int buf = decltype(buf_c)::value;
-        if (kb + 2 < n_kv) load_block(kb + 2, (buf + 2) % kFaBufs);
-        if (kb < wave_nkv) compute_block(kb, buf_c);
-        if (kb + 2 < n_kv) __builtin_amdgcn_s_waitcnt(kVmcntKeep);   // loads of kb + 2 stay in flight
-        else __builtin_amdgcn_s_waitcnt(0);
-        barrier();
-    };
-    load_block(0, 0);
-    if (n_kv > 1) load_block(1, 1);
-    if (n_kv > 1) __builtin_amdgcn_s_waitcnt(kVmcntKeep);
-    else __builtin_amdgcn_s_waitcnt(0);
-    barrier();
-    for (int kb = 0; kb < n_kv; kb += kFaBufs) {
-        step(kb, std::integral_constant<int, 0>{});
-        if (kb + 1 < n_kv) step(kb + 1, std::integral_constant<int, 1>{});
-        if (kb + 2 < n_kv) step(kb + 2, std::integral_constant<int, 2>{});
-    }
-    if (!active) return;
-
-    // Normalize and store: lane (row, j) holds dims NB (4 j + jj) + nb of its row.
+    // Normalize and store the current item's rows: lane (row, j) holds dims
+    // NB (4 j + jj) + nb of its row.
+    auto finish = [&](const FaItem& it) {
+        if (!active) return;
 #pragma unroll
-    for (int qt = 0; qt < kFaTiles; ++qt) {
-        const int row = qa + 16 * qt + m16;
-        float lt = l[qt] + __shfl_xor(l[qt], 16);
-        lt += __shfl_xor(lt, 32);
-        if (row >= L) continue;
-        const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-        const int64_t tok = s0 + row;
-        uint8_t* orow = a.out + tok * q_row + (int64_t)hq * kD * 2;
+        for (int qt = 0; qt < kFaTiles; ++qt) {
+            const int row = qa + 16 * qt + m16;
+            const float lt = sum_across_rows(l[qt]);
+            if (row >= it.L) continue;
+            const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+            const int64_t tok = (int64_t)it.s0 + row;
+            uint8_t* orow = a.out + tok * q_row + (int64_t)hq * kD * 2;
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-            const int d0 = NB * (4 * j + jj);
-            uint32_t wv[NB / 2];
+            for (int jj = 0; jj < 4; ++jj) {
+                const int d0 = NB * (4 * j + jj);
+                uint32_t wv[NB / 2];
 #pragma unroll
-            for (int w = 0; w < NB / 2; ++w) {
-                const float y0 = o[qt][2 * w][jj] * inv, y1 = o[qt][2 * w + 1][jj] * inv;
-                wv[w] = kF16 ? (f16_bits(y0) | (f16_bits(y1) << 16)) : (bf16_bits(y0) | (bf16_bits(y1) << 16));
+                for (int w = 0; w < NB / 2; ++w) wv[w] = pack2<kF16>(o[qt][2 * w][jj] * inv, o[qt][2 * w + 1][jj] * inv);
+                if constexpr (NB == 8) {
+                    *reinterpret_cast<u32x4_t*>(orow + d0 * 2) = u32x4_t{wv[0], wv[1], wv[2], wv[3]};
+                } else {
+                    *reinterpret_cast<uint2*>(orow + d0 * 2) = make_uint2(wv[0], wv[1]);
+                }
             }
-            if constexpr (NB == 8) {
-                *reinterpret_cast<u32x4_t*>(orow + d0 * 2) = u32x4_t{wv[0], wv[1], wv[2], wv[3]};
-            } else {
-                *reinterpret_cast<uint2*>(orow + d0 * 2) = make_uint2(wv[0], wv[1]);
-            }
+            if (j == 0) a.lse[tok * a.hq + hq] = (m[qt] + __builtin_log2f(lt)) * kLn2;
         }
-        if (j == 0) a.lse[tok * a.hq + hq] = (m[qt] + __builtin_log2f(lt)) * kLn2;
+    };
+
+    // Block stream. The blocks of the workgroup's items form one sequence; block g
+    // uses LDS buffer g % 3. Step g: the QK product of block g, the loads of block
+    // g + 2 (the load cursor; into the buffer of block g - 1, free since the last
+    // barrier), the rest of block g, then a wait for this wave's loads of block g + 1
+    // and the barrier, which publishes block g + 1 and ends every read of buffer
+    // g % 3 before step g + 1 loads block g + 3 into it. At an item's last block the
+    // wave issues the Q loads of its next item after the QK product (the last use of
+    // the current Q operands), so they arrive while the block finishes and the item
+    // is stored. The block loads come after the QK product because the compiler waits
+    // for all older vector-memory operations before the first use of new Q operands.
+    //
+    // s_waitcnt immediates (vmcnt = n, expcnt at its maximum, lgkmcnt 0).
+    constexpr int kW0 = (7 << 4);
+    constexpr int kWBlock = (kBlockLoads & 15) | (7 << 4) | (((kBlockLoads >> 4) & 3) << 14);
+    constexpr int kWQ = (kQLoads & 15) | (7 << 4) | (((kQLoads >> 4) & 3) << 14);
+    constexpr int kWBoth = ((kBlockLoads + kQLoads) & 15) | (7 << 4) | ((((kBlockLoads + kQLoads) >> 4) & 3) << 14);
+    auto step = [&](auto buf_c) -> bool {
+        constexpr int buf = decltype(buf_c)::value;
+        const bool last = ckb + 1 == ci.n_kv;
+        int32_t nk = ck + 1;
+        FaItem ni = ci;
+        const bool next = last && fa_item(a, sc, nk, ni);
+        const bool compute = ckb < wave_nkv;
+        if (compute) qk(buf_c);
+        const bool loaded = load_next((buf + 2) % kFaBufs);
+        if (next) load_q(ni);
+        if (compute) {
+            softmax(ckb, ci.L);
+            pv(buf_c);
+        }
+        if (loaded) {
+            if (next) __builtin_amdgcn_s_waitcnt(kWBoth);
+            else __builtin_amdgcn_s_waitcnt(kWBlock);
+        } else {
+            if (next) __builtin_amdgcn_s_waitcnt(kWQ);
+            else __builtin_amdgcn_s_waitcnt(kW0);
+        }
+        barrier();
+        if (!last) {
+            ++ckb;
+            return true;
+        }
+        finish(ci);
+        if (!next) return false;
+        ck = nk;
+        ci = ni;
+        ckb = 0;
+        enter(ci);
+        return true;
+    };
+
+    // Prologue: blocks 0 and 1 and the first item's Q, all complete before block 0.
+    const bool loaded1 = load_next(0) && load_next(1);
+    (void)loaded1;
+    load_q(ci);
+    enter(ci);
+    __builtin_amdgcn_s_waitcnt(kW0);
+    barrier();
+    for (;;) {
+        if (!step(std::integral_constant<int, 0>{})) break;
+        if (!step(std::integral_constant<int, 1>{})) break;
+        if (!step(std::integral_constant<int, 2>{})) break;
     }
+}
+
+// Compute units of the current device (cached per device id).
+int fa_device_cus() {
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    if (cus[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
 }
 
 template <int IT>
@@ -789,16 +970,23 @@ extern "C" int kvfp8_prefill_attention(const void* q, const void* k, const void*
     if ((dtype == KVFP8_BF16 || dtype == KVFP8_F16) && (head_dim == 64 || head_dim == 128)) {
         a.rows = kFaRows * kFaWaves / a.heads_per_block;
         a.qblocks = (max_seq_len + a.rows - 1) / a.rows;
-        const int64_t items = (int64_t)a.qblocks * batch * num_kv_heads * a.blocks_per_kv;
-        const int64_t per_xcd = (items + kXcds - 1) / kXcds;
-        if (per_xcd * kXcds >= ((int64_t)1 << 31)) return KVFP8_ESHAPE;
-        const dim3 grid((unsigned)(per_xcd * kXcds)), block(kFaThreads);
+        // One persistent workgroup per CU (its LDS holds one), per_xcd of them on
+        // each XCD, each walking its share of the XCD's items.
+        const int64_t units = (int64_t)batch * num_kv_heads * a.blocks_per_kv;
+        const int64_t upx = (units + kXcds - 1) / kXcds;
+        const int64_t items_per_xcd = upx * (int64_t)a.qblocks;
+        if (total_tokens >= ((int64_t)1 << 31) || upx * kXcds * (int64_t)a.qblocks >= ((int64_t)1 << 31))
+            return KVFP8_ESHAPE;
+        int64_t per_xcd = fa_device_cus() / kXcds;
+        per_xcd = per_xcd < 1 ? 1 : per_xcd;
+        per_xcd = per_xcd < items_per_xcd ? per_xcd : items_per_xcd;
+        const dim3 grid((unsigned)(kXcds * per_xcd)), block(kFaThreads);
         if (dtype == KVFP8_BF16) {
-            if (head_dim == 64) hipLaunchKernelGGL((prefill_fa_kernel<1, false>), grid, block, 0, s, a, items, per_xcd);
-            else hipLaunchKernelGGL((prefill_fa_kernel<2, false>), grid, block, 0, s, a, items, per_xcd);
+            if (head_dim == 64) hipLaunchKernelGGL((prefill_fa_kernel<1, false>), grid, block, 0, s, a, (int32_t)units, (int32_t)upx, (int32_t)per_xcd);
+            else hipLaunchKernelGGL((prefill_fa_kernel<2, false>), grid, block, 0, s, a, (int32_t)units, (int32_t)upx, (int32_t)per_xcd);
         } else {
-            if (head_dim == 64) hipLaunchKernelGGL((prefill_fa_kernel<1, true>), grid, block, 0, s, a, items, per_xcd);
-            else hipLaunchKernelGGL((prefill_fa_kernel<2, true>), grid, block, 0, s, a, items, per_xcd);
+            if (head_dim == 64) hipLaunchKernelGGL((prefill_fa_kernel<1, true>), grid, block, 0, s, a, (int32_t)units, (int32_t)upx, (int32_t)per_xcd);
+            else hipLaunchKernelGGL((prefill_fa_kernel<2, true>), grid, block, 0, s, a, (int32_t)units, (int32_t)upx, (int32_t)per_xcd);
         }
         return (int)hipGetLastError();
     }
