@@ -477,20 +477,13 @@ constexpr int kXcds = 8;           // workgroups are dispatched round-robin over
 constexpr int kGroupUnits = 8;     // units per longest-first group (their K/V: 8 x 512 KB at L 1024, D 128)
 constexpr int kFaBufs = 3;         // K/V block buffers in LDS
 
-// Wave-uniform loads through the scalar data cache, waited for at once. The
-// compiler would issue a vector load for a plain load of this memory (the kernel
-// also stores to global memory) and then wait for every vector-memory operation in
-// flight, K/V prefetches included.
-__device__ __forceinline__ int64_t uniform_load_i64(const int64_t* p) {
-    uint64_t v;
-    __asm__ volatile("s_load_dwordx2 %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p) : "memory");
-    return (int64_t)v;
-}
-__device__ __forceinline__ int32_t uniform_load_i32(const int32_t* p) {
-    uint32_t v;
-    __asm__ volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p) : "memory");
-    return (int32_t)v;
-}
+// Wave-uniform loads through the scalar data cache: a pointer into the constant
+// address space (read-only for the kernel's lifetime) lets the compiler use
+// s_load. A plain load of this memory would be a vector load here (the kernel also
+// stores to global memory), and the compiler would then wait for every
+// vector-memory operation in flight, K/V prefetches included.
+typedef __attribute__((address_space(4))) const int64_t* const_i64_ptr;
+typedef __attribute__((address_space(4))) const int32_t* const_i32_ptr;
 
 // One work item: query block qb of a unit (sequence b, KV head hk, head block hb).
 struct FaItem {
@@ -531,11 +524,13 @@ __device__ __forceinline__ bool fa_item(const PrefillArgs& a, const FaSchedule& 
         const int32_t rest = unit - b * a.hkv * a.blocks_per_kv;
         int64_t s0, s1;
         if (a.cu64) {
-            s0 = uniform_load_i64(reinterpret_cast<const int64_t*>(a.cu) + b);
-            s1 = uniform_load_i64(reinterpret_cast<const int64_t*>(a.cu) + b + 1);
+            const const_i64_ptr cu = (const_i64_ptr)a.cu;
+            s0 = cu[b];
+            s1 = cu[b + 1];
         } else {
-            s0 = uniform_load_i32(reinterpret_cast<const int32_t*>(a.cu) + b);
-            s1 = uniform_load_i32(reinterpret_cast<const int32_t*>(a.cu) + b + 1);
+            const const_i32_ptr cu = (const_i32_ptr)a.cu;
+            s0 = cu[b];
+            s1 = cu[b + 1];
         }
         s0 = s0 < 0 ? 0 : s0;
         s1 = s1 > a.total_tokens ? a.total_tokens : s1;
@@ -608,7 +603,9 @@ prefill_fa_kernel(PrefillArgs a, int32_t units, int32_t upx, int32_t per_xcd) {
     FaItem ci = li;
     int ckb = 0;
 
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    // The wave index as a wave-uniform (scalar) value, so that branches on it and on
+    // what derives from it are scalar branches.
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int m16 = lane & 15, j = lane >> 4;
     const int G = a.hq / a.hkv;
     const int gw = a.heads_per_block;
@@ -677,15 +674,24 @@ prefill_fa_kernel(PrefillArgs a, int32_t units, int32_t upx, int32_t per_xcd) {
     // Per-lane byte offsets of the operand reads (key tile bases are multiples of 16
     // rows, which the swizzle ignores: (16 t + r) % CPR = r % CPR):
     //   K operand, 32-dim step s: row m16, chunk 4 s + j;
-    //   V rows of key 16 t + 4 j + e (e < 4): the NB dims at NB m16.
-    int k_off[KS], v_off[4];
+    //   V^T operand, dims 16 nb .. + 15: the transposing LDS read (ds_read_b64_tr_b16)
+    //   gives lane i of each 16-lane group element i % 4 of the 8 bytes read by lane
+    //   4 r + i / 4 (r = 0..3). Lane (j, m16) therefore reads dims 16 nb + 4 (m16 % 4)
+    //   .. + 3 of key row 4 j + m16 / 4 of a 16-key tile and receives
+    //   V[4 j + r][16 nb + m16]: four keys of its dim, in the P^T operand's key order.
+    int k_off[KS], vt_off[NB];
 #pragma unroll
     for (int s = 0; s < KS; ++s) k_off[s] = m16 * ROW + 16 * ((4 * s + j) ^ (m16 % CPR));
+    {
+        const int vrow = 4 * j + (m16 >> 2);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int r = 4 * j + e;
-        v_off[e] = r * ROW + 16 * (((NB * m16) >> 3) ^ (r % CPR)) + ((NB * m16 * 2) & 15);
+        for (int nb = 0; nb < NB; ++nb)
+            vt_off[nb] = vrow * ROW + 16 * ((2 * nb + ((m16 >> 1) & 1)) ^ (vrow % CPR)) + 8 * (m16 & 1);
     }
+    typedef __attribute__((address_space(3))) const uint8_t lds_u8;
+    typedef short s16x4_t __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) s16x4_t lds_s16x4;
+    lds_u8* const v_lds = (lds_u8*)(&lds_v[0][0]);
 
     // Compute state of the current item: accumulators o[qt][nb] for the head dims;
     // l[qt] holds a lane's part (16 of every 64 keys) of its row's float32
@@ -778,42 +784,30 @@ prefill_fa_kernel(PrefillArgs a, int32_t units, int32_t upx, int32_t per_xcd) {
                 for (int w = 0; w < 4; ++w) pop[qt][pp][w] = pack2<kF16>(pr[8 * pp + 2 * w], pr[8 * pp + 2 * w + 1]);
         }
     };
-    // The lane reads NB dims at NB (l % 16) of the eight V rows of its keys; row
-    // pairs are transposed into one operand per dim, which feeds both row tiles.
+    // V^T operands straight from the transposing reads: half h of pair pp covers the
+    // keys of tile 2 pp + h. Each operand feeds both row tiles.
     auto pv = [&](auto buf_c) {
         constexpr int buf = decltype(buf_c)::value;
-        const uint8_t* vl = lds_v[buf];
 #pragma unroll
         for (int pp = 0; pp < 2; ++pp) {
-            constexpr int VW = NB / 2;       // dwords per row and lane
-            uint32_t rowv[8][VW];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                // Key 16 (2 pp + i / 4) + 4 j + i % 4.
-                const uint8_t* p = vl + 16 * (2 * pp + (i >> 2)) * ROW + v_off[i & 3];
-                if constexpr (VW == 4) {
-                    const u32x4_t x = *reinterpret_cast<const u32x4_t*>(p);
-#pragma unroll
-                    for (int w = 0; w < 4; ++w) rowv[i][w] = x[w];
-                } else {
-                    const uint2 x = *reinterpret_cast<const uint2*>(p);
-                    rowv[i][0] = x.x;
-                    rowv[i][1] = x.y;
-                }
-            }
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) {
-                const uint32_t sel = (nb & 1) ? 0x07060302u : 0x05040100u;
                 u32x4_t av;
 #pragma unroll
-                for (int q = 0; q < 4; ++q) av[q] = __builtin_amdgcn_perm(rowv[2 * q + 1][nb >> 1], rowv[2 * q][nb >> 1], sel);
+                for (int h = 0; h < 2; ++h) {
+                    const s16x4_t x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (lds_s16x4*)(v_lds + buf * (kKeys * ROW) + 16 * (2 * pp + h) * ROW + vt_off[nb]));
+                    const uint2 w = __builtin_bit_cast(uint2, x);
+                    av[2 * h] = w.x;
+                    av[2 * h + 1] = w.y;
+                }
 #pragma unroll
                 for (int qt = 0; qt < kFaTiles; ++qt) o[qt][nb] = mma16<kF16>(av, pop[qt][pp], o[qt][nb]);
             }
         }
     };
     // Normalize and store the current item's rows: lane (row, j) holds dims
-    // NB (4 j + jj) + nb of its row.
+    // 16 nb + 4 j + jj of its row (tile nb of the V^T operand covers dims 16 nb ..).
     auto finish = [&](const FaItem& it) {
         if (!active) return;
 #pragma unroll
@@ -825,16 +819,11 @@ prefill_fa_kernel(PrefillArgs a, int32_t units, int32_t upx, int32_t per_xcd) {
             const int64_t tok = (int64_t)it.s0 + row;
             uint8_t* orow = a.out + tok * q_row + (int64_t)hq * kD * 2;
 #pragma unroll
-            for (int jj = 0; jj < 4; ++jj) {
-                const int d0 = NB * (4 * j + jj);
-                uint32_t wv[NB / 2];
-#pragma unroll
-                for (int w = 0; w < NB / 2; ++w) wv[w] = pack2<kF16>(o[qt][2 * w][jj] * inv, o[qt][2 * w + 1][jj] * inv);
-                if constexpr (NB == 8) {
-                    *reinterpret_cast<u32x4_t*>(orow + d0 * 2) = u32x4_t{wv[0], wv[1], wv[2], wv[3]};
-                } else {
-                    *reinterpret_cast<uint2*>(orow + d0 * 2) = make_uint2(wv[0], wv[1]);
-                }
+            for (int nb = 0; nb < NB; ++nb) {
+                const int d0 = 16 * nb + 4 * j;
+                *reinterpret_cast<uint2*>(orow + d0 * 2) =
+                    make_uint2(pack2<kF16>(o[qt][nb][0] * inv, o[qt][nb][1] * inv),
+                               pack2<kF16>(o[qt][nb][2] * inv, o[qt][nb][3] * inv));
             }
             if (j == 0) a.lse[tok * a.hq + hq] = (m[qt] + __builtin_log2f(lt)) * kLn2;
         }
