@@ -95,19 +95,27 @@ class Setup:
         cache.append_kv(self.w.new_blocks, self.w.new_offsets, k, v)
         return decode_attention_wrapper(self.w.q, cache, self.context)
 
-    def capture(self):
-        """One HIP graph per pool holding that pool's whole step (append, decode,
-        combine), as a serving loop captures its decode step."""
+    def capture(self, steps: int):
+        """HIP graphs holding whole steps (append, decode, combine), one step per pool
+        in pool order, as a multi-layer model captures its decode step (each layer on
+        its own cache; the cfg5 leg captures all 16 layers the same way). Returns
+        (graph of num_pools steps, graph of steps % num_pools steps or None): replaying
+        the first steps // num_pools times and the second once runs exactly `steps`
+        steps."""
         import torch as t
 
-        graphs = []
-        for i in range(self.num_pools):
+        def graph_of(n):
             g = t.cuda.CUDAGraph()
             with t.cuda.graph(g):
-                self.step(i)
-            graphs.append(g)
+                for i in range(n):
+                    self.step(i)
+            return g
+
+        full = graph_of(self.num_pools)
+        rest = steps % self.num_pools
+        tail = graph_of(rest) if rest else None
         t.cuda.synchronize()
-        return graphs
+        return full, tail
 
 
 class _NoGC:
@@ -124,7 +132,8 @@ class _NoGC:
 
 def time_steps(setup: Setup, steps: int, warmup: int):
     """Three timed regions of `steps` calls each, after `warmup` eager steps:
-      * graph replay of the whole step (no host work between steps): ms per step;
+      * graph replay of whole steps, num_pools steps per graph (no host work between
+        steps, one graph launch per num_pools steps): ms per step;
       * the split (decode) kernel alone, `steps` launches back to back on the
         current stream between two HIP events, pools rotating: its mean launch
         duration, the figure the roofline divides by;
@@ -140,19 +149,22 @@ def time_steps(setup: Setup, steps: int, warmup: int):
     for i in range(warmup):
         setup.step(i)
     t.cuda.synchronize()
-    graphs = setup.capture()
-    for g in graphs:
-        g.replay()
+    full, tail = setup.capture(steps)
+    full.replay()
+    if tail is not None:
+        tail.replay()
     t.cuda.synchronize()
     start, end = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
     with _NoGC():
         start.record()
-        for i in range(steps):
-            graphs[i % len(graphs)].replay()
+        for _ in range(steps // setup.num_pools):
+            full.replay()
+        if tail is not None:
+            tail.replay()
         end.record()
         t.cuda.synchronize()
     graph_ms = start.elapsed_time(end) / steps
-    del graphs
+    del full, tail
 
     calls = [prepare_decode(setup.w.q, cache, setup.context) for cache in setup.caches]
     for c in calls:
@@ -555,6 +567,8 @@ def main():
                          f"page {s.block_size}, contexts {min(s.lengths)}..{max(s.lengths)} "
                          f"(total {s.total_tokens} KV tokens), FP8 e4m3fn paged cache with per-(page slot, "
                          f"kv head) scales, shuffled page pool; step = 1-token quantized append + decode"),
+            "timing": (f"steps replayed from HIP graphs of {main_result['pools']} steps, one per cache pool "
+                       "(as a multi-layer model's decode step graph holds one step per layer)"),
             "pools_rotated": main_result["pools"],
             "pool_mb": round(main_result["pool_mb"], 1),
         },
