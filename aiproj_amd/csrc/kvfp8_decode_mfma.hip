@@ -60,7 +60,7 @@ typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kMaxWaves = 8;            // KV heads served by one workgroup at a time
 constexpr int kMaxThreads = 64 * kMaxWaves;
-constexpr int kMinTilesPerGroup = 8;    // a workgroup gets at least 128 tokens per head
+constexpr int kMinTilesPerGroup = 2;    // a group gets at least 32 tokens per head
 constexpr int kWavesPerCu = 16;         // target waves resident per CU (caps the grid)
 constexpr int kMfmaMaxBatch = 8191;     // LDS: tile prefix (batch + 1) and sequence metadata (batch) int32
 
