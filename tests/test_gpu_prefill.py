@@ -115,6 +115,42 @@ def test_unwritten_rows_truncation_and_int64_offsets():
 
 
 @t.inference_mode()
+@pytest.mark.parametrize("dtype,head_dim", [(t.bfloat16, 128), (t.float16, 64)])
+def test_large_ragged_batch_over_persistent_workgroups(dtype, head_dim):
+    """Many sequences: the 16-bit kernel's persistent workgroups walk several items each,
+    its per-XCD unit ranges end in partial groups (152 units: 19 per XCD, in groups of
+    8, 8 and 3), zero-length
+    sequences and query blocks past a short sequence's end are skipped, and the longest
+    sequence is cut at max_seq_len (its later rows stay unwritten)."""
+    hq, hkv = 8, 2
+    rng = np.random.default_rng(36)
+    lengths = [int(x) for x in rng.integers(0, 300, size=74)] + [0, 900]
+    lengths[5] = 0
+    max_len = 640
+    q, k, v, cu = packed_inputs(lengths, hq, hkv, head_dim, dtype, seed=36)
+    total = q.shape[0]
+    scale = 1.0 / math.sqrt(head_dim)
+    out = t.full_like(q, 5.0)
+    lse = t.full((total, hq), -2.0, device="cuda")
+    rc = _native.lib().kvfp8_prefill_attention(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), _native.BF16 if dtype == t.bfloat16 else _native.F16, total,
+        hq, hkv, head_dim, cu.data_ptr(), _native.I32, len(lengths), max_len, scale, out.data_ptr(), lse.data_ptr(),
+        _native.stream_handle(q.device))
+    _native.check(rc, "kvfp8_prefill_attention")
+    t.cuda.synchronize()
+    want, want_lse = oracle_of(q, k, v, cu, max_len, scale)
+    written = ~np.isnan(want[:, 0, 0])
+    assert written.sum() == sum(min(n, max_len) for n in lengths)
+    got = out.double().cpu().numpy()
+    tol = TOLERANCE[dtype]
+    np.testing.assert_allclose(got[written], want[written], rtol=tol, atol=tol)
+    assert (got[~written] == 5.0).all()
+    got_lse = lse.double().cpu().numpy()
+    np.testing.assert_allclose(got_lse[written], want_lse[written], rtol=LSE_TOLERANCE, atol=LSE_TOLERANCE)
+    assert (got_lse[~written] == -2.0).all()
+
+
+@t.inference_mode()
 def test_config5_prefill_shape_against_float32_torch():
     """Config-5 prompts (1024 tokens, 16q/4kv, D 128, bf16), four sequences of the 64."""
     from aiproj_amd.model.transformer import prefill_attention
