@@ -119,9 +119,9 @@ def test_unwritten_rows_truncation_and_int64_offsets():
 def test_large_ragged_batch_over_persistent_workgroups(dtype, head_dim):
     """Many sequences: the 16-bit kernel's persistent workgroups walk several items each,
     its per-XCD unit ranges end in partial groups (152 units: 19 per XCD, in groups of
-    8, 8 and 3), zero-length
-    sequences and query blocks past a short sequence's end are skipped, and the longest
-    sequence is cut at max_seq_len (its later rows stay unwritten)."""
+    8, 8 and 3), zero-length sequences and query blocks past a short sequence's end are
+    skipped, and the longest sequence is cut at max_seq_len (its later rows stay
+    unwritten)."""
     hq, hkv = 8, 2
     rng = np.random.default_rng(36)
     lengths = [int(x) for x in rng.integers(0, 300, size=74)] + [0, 900]
