@@ -758,12 +758,14 @@ prefill_fa_kernel(PrefillArgs a, int32_t units, int32_t upx, int32_t per_xcd) {
             float mx = sc_[0];
 #pragma unroll
             for (int i = 1; i < 16; ++i) mx = fmaxf(mx, sc_[i]);
-            mx = max_across_rows(mx) * a.scale_log2;   // base-2 units (scale > 0 keeps the order)
+            mx *= a.scale_log2;                        // base-2 units (scale > 0 keeps the order)
             // Lazy rescale: the accumulators keep a reference max m that is only moved
             // when some row's max grows by more than 2^8 (p <= 256 meanwhile, far
             // inside float32 and bf16 range), so the accumulators are rarely scaled.
+            // Each lane tests its own 16 keys; only a rescale needs the row's max over
+            // its four lanes.
             if (__ballot(mx > m[qt] + 8.0f)) {
-                const float m_new = fmaxf(m[qt], mx);
+                const float m_new = fmaxf(m[qt], max_across_rows(mx));
                 const float m_use = m_new == kNegInf ? 0.0f : m_new;
                 const float alpha = __builtin_amdgcn_exp2f(m[qt] - m_use);
                 l[qt] *= alpha;
