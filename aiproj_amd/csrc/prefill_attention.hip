@@ -619,6 +619,9 @@ prefill_fa_kernel(PrefillArgs a, int32_t units, int32_t upx, int32_t per_xcd) {
     // otherwise assume that any LDS read may alias an LDS write in flight and wait
     // for every outstanding load before it (defeating the prefetch). The kernel
     // waits for them itself: the s_waitcnt before each block's closing barrier.
+    // They set m0 (the LDS destination) themselves. The compiler reserves m0 and
+    // writes it right before each instruction of its own that reads it, so it
+    // holds no value across these statements (and a clobber list may not name it).
     auto load_block = [&](const FaItem& it, int kb, int buf) {
 #pragma unroll
         for (int i = 0; i < CPT; ++i) {
