@@ -563,11 +563,14 @@ prefill_fa_kernel(PrefillArgs a, int32_t units, int32_t upx, int32_t per_xcd) {
     // for its Q operands of one item.
     constexpr int kBlockLoads = 2 * CPT;
     constexpr int kQLoads = kFaTiles * KS;
+    // Every lambda below is forced inline: a call would keep its captures (the
+    // accumulator arrays among them) in scratch memory.
+    //
     // Workgroup barrier that does not drain the K/V prefetch: __syncthreads() would
     // wait for every outstanding load. Before it the wave waits (s_waitcnt) for its
     // LDS reads and for its loads older than the ones it keeps in flight; the
     // compiler-level fences keep every LDS access on its side of the barrier.
-    auto barrier = [&]() {
+    auto barrier = [&]() __attribute__((always_inline)) {
         __asm__ volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         __asm__ volatile("" ::: "memory");
@@ -622,7 +625,7 @@ prefill_fa_kernel(PrefillArgs a, int32_t units, int32_t upx, int32_t per_xcd) {
     // They set m0 (the LDS destination) themselves. The compiler reserves m0 and
     // writes it right before each instruction of its own that reads it, so it
     // holds no value across these statements (and a clobber list may not name it).
-    auto load_block = [&](const FaItem& it, int kb, int buf) {
+    auto load_block = [&](const FaItem& it, int kb, int buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < CPT; ++i) {
             const int c = threadIdx.x + kFaThreads * i;         // slot written by this lane
@@ -642,7 +645,7 @@ prefill_fa_kernel(PrefillArgs a, int32_t units, int32_t upx, int32_t per_xcd) {
     };
     // Load the load cursor's block into `buf` and advance the cursor; false when
     // every block has been loaded. Every wave issues the same loads.
-    auto load_next = [&](int buf) -> bool {
+    auto load_next = [&](int buf) __attribute__((always_inline)) -> bool {
         if (!lhas) return false;
         load_block(li, lkb, buf);
         if (++lkb == li.n_kv) {
@@ -654,15 +657,15 @@ prefill_fa_kernel(PrefillArgs a, int32_t units, int32_t upx, int32_t per_xcd) {
     };
 
     // This wave's rows of an item: q head hq, query rows qa .. qa + 31.
-    auto wave_head = [&](const FaItem& it) { return it.hk * G + it.hb * gw + wave % gw; };
-    auto wave_row = [&](const FaItem& it) { return it.qb * a.rows + kFaRows * (wave / gw); };
+    auto wave_head = [&](const FaItem& it) __attribute__((always_inline)) { return it.hk * G + it.hb * gw + wave % gw; };
+    auto wave_row = [&](const FaItem& it) __attribute__((always_inline)) { return it.qb * a.rows + kFaRows * (wave / gw); };
 
     // Q^T operands: lane (row 16 qt + l % 16, l / 16) holds dims 32 s + 8 (l / 16) .. + 7.
     // Rows past the sequence load its last row: their results are never stored, and
     // every row's softmax is its own, so they need no zeroing (which would have to
     // wait for the loads where they are issued).
     u32x4_t qop[kFaTiles][KS];
-    auto load_q = [&](const FaItem& it) {
+    auto load_q = [&](const FaItem& it) __attribute__((always_inline)) {
         const int hq_n = wave_head(it), qa_n = wave_row(it);
 #pragma unroll
         for (int qt = 0; qt < kFaTiles; ++qt) {
@@ -703,7 +706,7 @@ prefill_fa_kernel(PrefillArgs a, int32_t units, int32_t upx, int32_t per_xcd) {
     float m[kFaTiles], neg_m[kFaTiles], l[kFaTiles];
     int hq = 0, qa = 0, wave_nkv = 0;
     bool active = false;
-    auto enter = [&](const FaItem& it) {
+    auto enter = [&](const FaItem& it) __attribute__((always_inline)) {
         hq = wave_head(it);
         qa = wave_row(it);
         active = qa < it.L;
@@ -724,7 +727,7 @@ prefill_fa_kernel(PrefillArgs a, int32_t units, int32_t upx, int32_t per_xcd) {
     // so all LDS operand addresses are a per-lane offset plus an immediate.
     f32x4_t sacc[4][kFaTiles];
     u32x4_t pop[kFaTiles][2];           // P^T operands; pp holds keys 16 (2 pp + i / 4) + 4 j + i % 4
-    auto qk = [&](auto buf_c) {
+    auto qk = [&](auto buf_c) __attribute__((always_inline)) {
         constexpr int buf = decltype(buf_c)::value;
         const uint8_t* kl = lds_k[buf];
         // 4 key tiles x 2 row tiles; each K operand feeds both row tiles.
@@ -739,7 +742,7 @@ prefill_fa_kernel(PrefillArgs a, int32_t units, int32_t upx, int32_t per_xcd) {
             }
         }
     };
-    auto softmax = [&](int kb, int L) {
+    auto softmax = [&](int kb, int L) __attribute__((always_inline)) {
         const bool full = kb * kKeys + kKeys - 1 <= qa && kb * kKeys + kKeys <= L;   // wave-uniform
 #pragma unroll
         for (int qt = 0; qt < kFaTiles; ++qt) {
@@ -791,7 +794,7 @@ prefill_fa_kernel(PrefillArgs a, int32_t units, int32_t upx, int32_t per_xcd) {
     };
     // V^T operands straight from the transposing reads: half h of pair pp covers the
     // keys of tile 2 pp + h. Each operand feeds both row tiles.
-    auto pv = [&](auto buf_c) {
+    auto pv = [&](auto buf_c) __attribute__((always_inline)) {
         constexpr int buf = decltype(buf_c)::value;
 #pragma unroll
         for (int pp = 0; pp < 2; ++pp) {
@@ -813,7 +816,7 @@ prefill_fa_kernel(PrefillArgs a, int32_t units, int32_t upx, int32_t per_xcd) {
     };
     // Normalize and store the current item's rows: lane (row, j) holds dims
     // 16 nb + 4 j + jj of its row (tile nb of the V^T operand covers dims 16 nb ..).
-    auto finish = [&](const FaItem& it) {
+    auto finish = [&](const FaItem& it) __attribute__((always_inline)) {
         if (!active) return;
 #pragma unroll
         for (int qt = 0; qt < kFaTiles; ++qt) {
@@ -850,7 +853,7 @@ prefill_fa_kernel(PrefillArgs a, int32_t units, int32_t upx, int32_t per_xcd) {
     constexpr int kWBlock = (kBlockLoads & 15) | (7 << 4) | (((kBlockLoads >> 4) & 3) << 14);
     constexpr int kWQ = (kQLoads & 15) | (7 << 4) | (((kQLoads >> 4) & 3) << 14);
     constexpr int kWBoth = ((kBlockLoads + kQLoads) & 15) | (7 << 4) | ((((kBlockLoads + kQLoads) >> 4) & 3) << 14);
-    auto step = [&](auto buf_c) -> bool {
+    auto step = [&](auto buf_c) __attribute__((always_inline)) -> bool {
         constexpr int buf = decltype(buf_c)::value;
         const bool last = ckb + 1 == ci.n_kv;
         int32_t nk = ck + 1;
