@@ -54,6 +54,7 @@ def parse_args():
     p.add_argument("--no-prefill", action="store_true", help="skip the prefill-size append and attention legs")
     p.add_argument("--no-model", action="store_true", help="skip the cfg5 model decode leg")
     p.add_argument("--no-others", action="store_true", help="skip the cfg1/cfg3/cfg4 decode legs")
+    p.add_argument("--no-sweep", action="store_true", help="skip the reference-style batch x context sweep")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     return p.parse_args()
 
@@ -177,7 +178,16 @@ def time_steps(setup: Setup, steps: int, warmup: int):
         end.record()
         t.cuda.synchronize()
     split_ms = start.elapsed_time(end) / steps
-    del calls
+    # The same launches one at a time, each between its own pair of events: the median.
+    pairs = [(t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    with _NoGC():
+        for i, (e0, e1) in enumerate(pairs):
+            e0.record()
+            calls[i % len(calls)].split()
+            e1.record()
+        t.cuda.synchronize()
+    split_median_ms = float(sorted(e0.elapsed_time(e1) for e0, e1 in pairs)[steps // 2])
+    del calls, pairs
 
     _native.check(lib.kvfp8_timing_enable(steps), "kvfp8_timing_enable")
     t.cuda.synchronize()
@@ -192,8 +202,8 @@ def time_steps(setup: Setup, steps: int, warmup: int):
     launches = ctypes.c_int64(0)
     _native.check(lib.kvfp8_timing_read(ctypes.byref(total_ms), ctypes.byref(launches)), "kvfp8_timing_read")
     dispatch_ms = total_ms.value / max(1, launches.value)
-    return {"graph_ms": graph_ms, "eager_ms": eager_ms, "split_ms": split_ms, "dispatch_ms": dispatch_ms,
-            "dispatch_launches": launches.value}
+    return {"graph_ms": graph_ms, "eager_ms": eager_ms, "split_ms": split_ms, "split_median_ms": split_median_ms,
+            "dispatch_ms": dispatch_ms, "dispatch_launches": launches.value}
 
 
 def prefill_write(steps: int):
@@ -360,6 +370,82 @@ def model_decode(steps: int):
     return out
 
 
+def reference_sweep(iterations: int = 50, warmup: int = 10):
+    """The reference's own decode benchmark (benchmarks/bench_kv_cache_fp8.py:38-158) on
+    this library: batch sizes {1, 8, 32} x context lengths {512, 2048, 8192}, 8 q / 4 KV
+    heads, D 64, page 16, one bf16 and one FP8 cache holding the same seeded K/V
+    history, q bf16. Each point times `iterations` eager `decode_attention_wrapper` calls
+    between two events after `warmup` calls, as the reference does (no pool rotation;
+    the smaller working sets stay in the 256 MB last-level cache, as in the reference's
+    own runs). Per dtype, a least-squares fit of time = overhead + kv_bytes / bandwidth
+    over the nine points, and the fp8-over-bf16 speedup per point."""
+    import torch as t
+    from aiproj_amd.inference.page_allocator import PageAllocator
+    from aiproj_amd.inference.paged_kv_cache import PagedKVCache
+    from aiproj_amd.kernals.decode_attention import decode_attention_wrapper
+
+    fp8 = t.float8_e4m3fn
+    hq, hkv, dim, bs = 8, 4, 64, 16
+    gen = t.Generator(device="cuda").manual_seed(11)
+
+    def per_token(cache):
+        per_vector = dim * cache.k.element_size() + (cache.k_scales.element_size() if cache.quantized else 0)
+        return 2 * hkv * per_vector
+
+    rows = []
+    with t.inference_mode():
+        for batch in (1, 8, 32):
+            for ctx in (512, 2048, 8192):
+                num_blocks = batch * (-(-ctx // bs)) + 1
+                manager = PageAllocator(num_blocks, bs, batch + 1, ctx + bs, "cuda")
+                caches = {d: PagedKVCache(num_blocks, bs, hkv, dim, "cuda", d) for d in (t.bfloat16, fp8)}
+                slots = []
+                for rid in range(batch):
+                    slots.append(manager.allocate_request(rid, ctx))
+                    k = t.randn(ctx, hkv, dim, device="cuda", dtype=t.bfloat16, generator=gen)
+                    v = t.randn(ctx, hkv, dim, device="cuda", dtype=t.bfloat16, generator=gen)
+                    for cache in caches.values():
+                        manager.append_request(rid, t.arange(ctx, device="cuda"), k, v, cache)
+                    manager.advance(rid, ctx - 1)
+                context = manager.create_container(t.tensor(slots, device="cuda"),
+                                                   t.arange(batch + 1, dtype=t.int32, device="cuda"),
+                                                   t.full((batch,), ctx - 1, device="cuda"))
+                q = t.randn(batch, hq, dim, device="cuda", dtype=t.bfloat16, generator=gen)
+                for dtype, cache in caches.items():
+                    for _ in range(warmup):
+                        decode_attention_wrapper(q, cache, context)
+                    t.cuda.synchronize()
+                    start, end = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+                    with _NoGC():
+                        start.record()
+                        for _ in range(iterations):
+                            decode_attention_wrapper(q, cache, context)
+                        end.record()
+                        t.cuda.synchronize()
+                    ms = start.elapsed_time(end) / iterations
+                    rows.append(("fp8" if dtype == fp8 else "bf16", batch, ctx, batch * ctx * per_token(cache), ms))
+                del caches, context, q, manager
+                t.cuda.empty_cache()
+    fits = {}
+    for name in ("bf16", "fp8"):
+        pts = [(kv, ms * 1e-3) for d, _, _, kv, ms in rows if d == name]
+        design = t.tensor([[1.0, float(kv)] for kv, _ in pts], dtype=t.float64)
+        seconds = t.tensor([[sec] for _, sec in pts], dtype=t.float64)
+        overhead, slope = t.linalg.lstsq(design, seconds).solution.flatten().tolist()
+        fits[name] = {"overhead_us": round(overhead * 1e6, 2),
+                      "bandwidth_gbs": round(1.0 / slope / 1e9, 1) if slope > 0 else None}
+    timing = {(d, b, c): ms for d, b, c, _, ms in rows}
+    points = [{"dtype": d, "batch": b, "context": c, "kv_mb": round(kv / 2 ** 20, 2), "us_per_call": round(ms * 1e3, 2),
+               "gbs": round(kv / (ms * 1e-3) / 1e9, 1)} for d, b, c, kv, ms in rows]
+    speedup = [{"batch": b, "context": c, "fp8_speedup": round(timing[("bf16", b, c)] / timing[("fp8", b, c)], 3)}
+               for b in (1, 8, 32) for c in (512, 2048, 8192)]
+    for name, f in fits.items():
+        log(f"[sweep] {name}: time = {f['overhead_us']:.1f} us + kv_bytes / {f['bandwidth_gbs']} GB/s")
+    return {"workload": "reference decode sweep: batch {1, 8, 32} x context {512, 2048, 8192}, 8q/4kv, D 64, "
+                        "page 16, eager decode_attention_wrapper calls (benchmarks/bench_kv_cache_fp8.py defaults)",
+            "fit": fits, "points": points, "speedup": speedup}
+
+
 def copy_bandwidth_gbs(nbytes: int = 2 * 2 ** 30) -> float:
     """Device-to-device copy of nbytes (read + write), the practical HBM roofline."""
     import torch as t
@@ -460,6 +546,7 @@ def measure(name: str, steps: int, warmup: int):
         "ms_per_step": ms,
         "eager_ms_per_step": eager_ms,
         "split_kernel_ms": kernel_ms,
+        "split_median_ms": times["split_median_ms"],
         "dispatch_kernel_ms": times["dispatch_ms"],
         "dispatch_launches": times["dispatch_launches"],
         "step_bytes": setup.decode_bytes + setup.append_bytes,
@@ -547,6 +634,7 @@ def main():
     prefill = None if args.no_prefill else prefill_write(max(10, args.steps // 2))
     prefill_attn = None if args.no_prefill else prefill_attention(max(10, args.steps // 2))
     model = None if args.no_model else model_decode(100)
+    sweep = None if args.no_sweep else reference_sweep()
     kernel_gbs = main_result["kernel_gbs"]
     line = {
         "metric": METRIC,
@@ -589,6 +677,7 @@ def main():
             "timing": (f"{args.steps} back-to-back launches of the decode kernel alone "
                        "(kvfp8_paged_decode_split, pools rotating) between two HIP events on its stream"),
             "dispatch_event_us": round(main_result["dispatch_kernel_ms"] * 1e3, 2),
+            "median_launch_us": round(main_result["split_median_ms"] * 1e3, 2),
         },
         "cpu_baseline": cpu,
         "secondary": secondary,
@@ -596,6 +685,7 @@ def main():
         "prefill_write": prefill,
         "prefill_attention": prefill_attn,
         "model_decode": model,
+        "reference_sweep": sweep,
     }
     print(json.dumps(line), flush=True)
 
