@@ -112,8 +112,16 @@ def ptr(tensor) -> int | None:
     return None if tensor is None else tensor.data_ptr()
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_handle(device: torch.device) -> int:
-    """The current HIP stream of `device`, as the raw handle the C ABI takes."""
+    """The current HIP stream of `device`, as the raw handle the C ABI takes. Read
+    straight from torch's stream state when it offers that (no Python stream object
+    per call, which costs about 2.5 µs), else through torch.cuda.current_stream."""
+    if _raw_stream is not None:
+        index = device.index if device.index is not None else torch.cuda.current_device()
+        return _raw_stream(index)
     return torch.cuda.current_stream(device).cuda_stream
 
 

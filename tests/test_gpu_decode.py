@@ -382,3 +382,31 @@ def test_split_then_reduce_equals_one_call(cache_dtype, head_dim):
     call.reduce()
     assert t.equal(call.output, whole)
     assert t.equal(whole[2], t.zeros_like(whole[2]))
+
+
+def test_launches_follow_the_current_stream():
+    """The handle passed to the C ABI is torch's current stream, default or not, and a
+    decode enqueued under another stream runs there (its output is ready once that
+    stream is synchronized)."""
+    from aiproj_amd import _native
+
+    dev = t.device("cuda")
+    assert _native.stream_handle(dev) == t.cuda.current_stream(dev).cuda_stream
+    side = t.cuda.Stream()
+    w = workloads.build(workloads.spec("cfg1"), "cuda")
+    cache = PagedKVCache(w.num_blocks, 16, w.spec.num_kv_heads, w.spec.head_dim, "cuda", FP8)
+    workloads.fill_cache(w, cache, "cuda")
+    k_new, v_new = workloads.new_kv(w, "cuda", 0)
+    cache.append_kv(w.new_blocks, w.new_offsets, k_new, v_new)
+    ctx = workloads.make_context(w)
+    want = decode_attention_wrapper(w.q, cache, ctx)
+    assert bool(t.isfinite(want).all())
+    t.cuda.synchronize()
+    side.wait_stream(t.cuda.current_stream())
+    with t.cuda.stream(side):
+        assert _native.stream_handle(dev) == side.cuda_stream
+        assert _native.stream_handle(t.device("cuda", t.cuda.current_device())) == side.cuda_stream
+        got = decode_attention_wrapper(w.q, cache, ctx)
+    side.synchronize()
+    assert t.equal(got, want)
+    assert _native.stream_handle(dev) == t.cuda.current_stream(dev).cuda_stream
