@@ -60,7 +60,7 @@ class GreedyDecoder:
         positions = t.arange(length, device=self.device).repeat(batch)
         cu = t.arange(batch + 1, device=self.device, dtype=t.int32) * length
         ctx = self.allocator.create_container(self.slots, cu, positions, validate=False)
-        meta = StepMeta("prefill", positions, ctx, seq_lens=[length] * batch)
+        meta = StepMeta("prefill", positions, ctx, cu_seqlens=cu, max_seqlen=length)
         logits = self.model(prompts.reshape(-1).to(self.device), meta, self.caches)
         self.allocator.advance_batch(list(range(batch)), [length] * batch)
         self.tokens.copy_(logits.argmax(-1))

@@ -20,19 +20,21 @@ dense SwiGLU, which is that MoE with one expert and top-1 routing (routing weigh
 What runs where: the norms (`rmsnorm_kernel`, residual add fused into the next
 norm), the cache write and the decode attention are this library's HIP kernels;
 the projections and the FFN are plain GEMMs (hipBLASLt through torch); prompt
-(prefill) attention runs in float32 PyTorch, chunked, with contiguous operands.
+(prefill) attention is the varlen causal HIP kernel behind `flash_attention_forward`,
+as the reference calls its FlashAttentionFunction there (`attention.py:103-110`).
 """
 
 from __future__ import annotations
 
 import math
-from dataclasses import dataclass, field
+from dataclasses import dataclass
 
 import torch as t
 from torch import nn
 from torch.nn import functional as F
 
 from aiproj_amd.kernals.decode_attention import decode_attention_wrapper
+from aiproj_amd.kernals.flash_attention import flash_attention_forward
 from aiproj_amd.model.rmsnorm import add_rmsnorm, rmsnorm_forward
 
 
@@ -58,7 +60,8 @@ class StepMeta:
     mode: str                          # "prefill" or "decode"
     token_positions: t.Tensor          # [T] int64, position of every packed token
     cache_context: object              # CacheContainer: slots, physical_blocks, block_offsets, ...
-    seq_lens: list[int] = field(default_factory=list)   # prefill only: host lengths of the packed prompts
+    cu_seqlens: t.Tensor | None = None  # prefill only: [B + 1] offsets of the packed prompts (device)
+    max_seqlen: int = 0                 # prefill only: longest prompt (host int)
 
 
 class RoPE(nn.Module):
@@ -98,39 +101,6 @@ class RoPE(nn.Module):
         return x
 
 
-def prefill_attention(q: t.Tensor, k: t.Tensor, v: t.Tensor, seq_lens: list[int],
-                      chunk_bytes: int = 1 << 30) -> t.Tensor:
-    """Causal GQA attention of packed prompts q [T, Hq, D], k/v [T, Hkv, D] -> [T, Hq, D].
-
-    Float32 math with contiguous operands, sequences of equal length batched
-    together in chunks whose score tensor stays under `chunk_bytes`."""
-    total, hq, d = q.shape
-    hkv = k.shape[1]
-    g = hq // hkv
-    out = t.empty_like(q)
-    start = 0
-    i = 0
-    while i < len(seq_lens):
-        length = seq_lens[i]
-        per_seq = hq * length * length * 4
-        n = 1
-        while (i + n < len(seq_lens) and seq_lens[i + n] == length and (n + 1) * per_seq <= chunk_bytes):
-            n += 1
-        end = start + n * length
-        qs = q[start:end].float().view(n, length, hkv, g, d).permute(0, 2, 3, 1, 4).contiguous()
-        ks = k[start:end].float().view(n, length, hkv, d).permute(0, 2, 3, 1).unsqueeze(2).contiguous()
-        vs = v[start:end].float().view(n, length, hkv, d).permute(0, 2, 1, 3).unsqueeze(2).contiguous()
-        scores = t.matmul(qs, ks) * (1.0 / math.sqrt(d))                      # [n, hkv, g, L, L]
-        causal = t.ones(length, length, dtype=t.bool, device=q.device).triu(1)
-        scores.masked_fill_(causal, float("-inf"))
-        probs = scores.softmax(dim=-1)
-        o = t.matmul(probs, vs)                                                # [n, hkv, g, L, d]
-        out[start:end] = o.permute(0, 3, 1, 2, 4).reshape(n * length, hq, d).to(q.dtype)
-        start = end
-        i += n
-    return out
-
-
 class Attention(nn.Module):
     def __init__(self, cfg: ModelConfig):
         super().__init__()
@@ -152,7 +122,10 @@ class Attention(nn.Module):
         v = qkv[:, self.q_dim + self.kv_dim:].view(-1, cfg.num_kv_heads, cfg.head_dim)
         ctx = meta.cache_context
         if meta.mode == "prefill":
-            out = prefill_attention(q, k, v, meta.seq_lens)
+            # The varlen causal HIP kernel (reference FlashAttentionFunction, `attention.py:103-110`).
+            # q, k and v are views into the fused projection; the kernel takes packed rows.
+            out, _ = flash_attention_forward(q.contiguous(), k.contiguous(), v.contiguous(), meta.cu_seqlens,
+                                             meta.max_seqlen, 1.0 / math.sqrt(cfg.head_dim))
             cache.append_kv(ctx.physical_blocks, ctx.block_offsets, k, v)
         else:
             cache.append_kv(ctx.physical_blocks, ctx.block_offsets, k, v)
@@ -214,6 +187,6 @@ class TransformerLM(nn.Module):
             x, h = add_rmsnorm(x, f, nxt, eps)
         if meta.mode == "prefill":
             # Only the last prompt token of each sequence is sampled from.
-            last = t.tensor(meta.seq_lens, device=h.device).cumsum(0) - 1
+            last = meta.cu_seqlens[1:].long() - 1
             h = h[last]
         return F.linear(h, self.embed.weight)

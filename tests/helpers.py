@@ -53,3 +53,37 @@ def brute_force_decode(q, k, v):
         for i in range(d):
             out[h][i] = sum(weights[t_] * v[t_][kv][i] for t_ in range(length)) / total
     return out
+
+
+def torch_prefill_attention(q: t.Tensor, k: t.Tensor, v: t.Tensor, seq_lens: list[int],
+                            chunk_bytes: int = 1 << 30) -> t.Tensor:
+    """Causal GQA attention of packed prompts q [T, Hq, D], k/v [T, Hkv, D] -> [T, Hq, D],
+    a float32 torch reference for the prefill kernel.
+
+    Float32 math with contiguous operands, sequences of equal length batched
+    together in chunks whose score tensor stays under `chunk_bytes`."""
+    total, hq, d = q.shape
+    hkv = k.shape[1]
+    g = hq // hkv
+    out = t.empty_like(q)
+    start = 0
+    i = 0
+    while i < len(seq_lens):
+        length = seq_lens[i]
+        per_seq = hq * length * length * 4
+        n = 1
+        while (i + n < len(seq_lens) and seq_lens[i + n] == length and (n + 1) * per_seq <= chunk_bytes):
+            n += 1
+        end = start + n * length
+        qs = q[start:end].float().view(n, length, hkv, g, d).permute(0, 2, 3, 1, 4).contiguous()
+        ks = k[start:end].float().view(n, length, hkv, d).permute(0, 2, 3, 1).unsqueeze(2).contiguous()
+        vs = v[start:end].float().view(n, length, hkv, d).permute(0, 2, 1, 3).unsqueeze(2).contiguous()
+        scores = t.matmul(qs, ks) * (1.0 / math.sqrt(d))                      # [n, hkv, g, L, L]
+        causal = t.ones(length, length, dtype=t.bool, device=q.device).triu(1)
+        scores.masked_fill_(causal, float("-inf"))
+        probs = scores.softmax(dim=-1)
+        o = t.matmul(probs, vs)                                                # [n, hkv, g, L, d]
+        out[start:end] = o.permute(0, 3, 1, 2, 4).reshape(n * length, hq, d).to(q.dtype)
+        start = end
+        i += n
+    return out

@@ -153,13 +153,13 @@ def test_large_ragged_batch_over_persistent_workgroups(dtype, head_dim):
 @t.inference_mode()
 def test_config5_prefill_shape_against_float32_torch():
     """Config-5 prompts (1024 tokens, 16q/4kv, D 128, bf16), four sequences of the 64."""
-    from aiproj_amd.model.transformer import prefill_attention
+    from tests.helpers import torch_prefill_attention
 
     lengths = [1024] * 4
     q, k, v, cu = packed_inputs(lengths, 16, 4, 128, t.bfloat16, seed=34)
     scale = 1.0 / math.sqrt(128)
     out, lse = flash_attention_forward(q, k, v, cu, 1024, scale)
-    want = prefill_attention(q, k, v, lengths).float()       # float32 math, contiguous operands
+    want = torch_prefill_attention(q, k, v, lengths).float()   # float32 math, contiguous operands
     t.testing.assert_close(out.float(), want, rtol=1.6e-2, atol=1.6e-2)
     qs = q[:1024].float().transpose(0, 1)
     ks = k[:1024].float().transpose(0, 1).repeat_interleave(4, 0)
