@@ -963,17 +963,21 @@ extern "C" int kvfp8_prefill_attention(const void* q, const void* k, const void*
     a.total_tokens = total_tokens;
     a.scale_log2 = scale * 1.44269504088896340736f;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    // 16-bit inputs with D 64 or 128: the wide-tile kernel.
-    if ((dtype == KVFP8_BF16 || dtype == KVFP8_F16) && (head_dim == 64 || head_dim == 128)) {
-        a.rows = kFaRows * kFaWaves / a.heads_per_block;
+    // 16-bit inputs with D 64 or 128: the wide-tile kernel, whose item and token
+    // indices are int32 (larger inputs take the general kernel below).
+    const int fa_rows = kFaRows * kFaWaves / a.heads_per_block;
+    const int64_t fa_units = (int64_t)batch * num_kv_heads * a.blocks_per_kv;
+    const int64_t fa_upx = (fa_units + kXcds - 1) / kXcds;
+    const bool fa_fits = total_tokens < ((int64_t)1 << 31) &&
+                         fa_upx * kXcds * (((int64_t)max_seq_len + fa_rows - 1) / fa_rows) < ((int64_t)1 << 31);
+    if ((dtype == KVFP8_BF16 || dtype == KVFP8_F16) && (head_dim == 64 || head_dim == 128) && fa_fits) {
+        a.rows = fa_rows;
         a.qblocks = (max_seq_len + a.rows - 1) / a.rows;
         // One persistent workgroup per CU (its LDS holds one), per_xcd of them on
         // each XCD, each walking its share of the XCD's items.
-        const int64_t units = (int64_t)batch * num_kv_heads * a.blocks_per_kv;
-        const int64_t upx = (units + kXcds - 1) / kXcds;
+        const int64_t units = fa_units;
+        const int64_t upx = fa_upx;
         const int64_t items_per_xcd = upx * (int64_t)a.qblocks;
-        if (total_tokens >= ((int64_t)1 << 31) || upx * kXcds * (int64_t)a.qblocks >= ((int64_t)1 << 31))
-            return KVFP8_ESHAPE;
         int64_t per_xcd = fa_device_cus() / kXcds;
         per_xcd = per_xcd < 1 ? 1 : per_xcd;
         per_xcd = per_xcd < items_per_xcd ? per_xcd : items_per_xcd;
