@@ -632,6 +632,9 @@ def main():
             }
             del r
     prefill = None if args.no_prefill else prefill_write(max(10, args.steps // 2))
+    if prefill is not None:
+        # Mixed read + write traffic: the device copy is its practical ceiling.
+        prefill["pct_of_copy"] = round(100 * prefill["achieved"] / copy_gbs, 2)
     prefill_attn = None if args.no_prefill else prefill_attention(max(10, args.steps // 2))
     model = None if args.no_model else model_decode(100)
     sweep = None if args.no_sweep else reference_sweep()
