@@ -77,10 +77,18 @@ def store_append(paged_kv_cache, ks, vs, physical_blocks, block_offsets):
     The device counterpart of reference `inference/paged_kv_cache.py:77-79`, one
     launch of `store_append_kernel` through `kvfp8_store_append`.
     """
-    num_blocks, block_size, num_kv_heads, head_dim = paged_kv_cache.k.shape
+    store_rows(paged_kv_cache.k, paged_kv_cache.v, ks, vs, physical_blocks, block_offsets, what="store_append")
+
+
+def store_rows(k_cache, v_cache, ks, vs, rows, cols, what="store_rows"):
+    """k_cache[rows[t], cols[t]] = ks[t] (and the same for V) for [R, C, H_kv, D] device caches.
+
+    One launch of `store_append_kernel`: the cache is addressed as R pages of C slots.
+    Entries with rows[t] outside [0, R) or cols[t] outside [0, C) are skipped.
+    """
+    num_blocks, block_size, num_kv_heads, head_dim = k_cache.shape
     num_tokens = ks.shape[0]
-    device = _native.require_gpu(ks, vs, physical_blocks, block_offsets, paged_kv_cache.k,
-                                 what="store_append")
+    device = _native.require_gpu(ks, vs, rows, cols, k_cache, what=what)
     if num_tokens == 0:
         return
     ks, vs = _prepare_input(ks), _prepare_input(vs)
@@ -90,11 +98,10 @@ def store_append(paged_kv_cache, ks, vs, physical_blocks, block_offsets):
     rc = lib.kvfp8_store_append(
         ks.data_ptr(), vs.data_ptr(), _native.dtype_code(ks.dtype),
         ks.stride(0), ks.stride(1), vs.stride(0), vs.stride(1),
-        physical_blocks.data_ptr(), _native.dtype_code(physical_blocks.dtype),
-        block_offsets.data_ptr(), _native.dtype_code(block_offsets.dtype),
+        rows.data_ptr(), _native.dtype_code(rows.dtype),
+        cols.data_ptr(), _native.dtype_code(cols.dtype),
         num_tokens, num_kv_heads, head_dim, num_blocks, block_size,
-        paged_kv_cache.k.data_ptr(), paged_kv_cache.v.data_ptr(),
-        _native.dtype_code(paged_kv_cache.k.dtype),
+        k_cache.data_ptr(), v_cache.data_ptr(), _native.dtype_code(k_cache.dtype),
         _native.stream_handle(device),
     )
     _native.check(rc, "kvfp8_store_append")

@@ -1,7 +1,8 @@
 """KVCacheConfig, PagedKVCache and PageAllocator host contracts (CPU).
 
 Mirrors sections B and C of reference tests/test_kv_cache_quantization.py:145-239
-and the allocator tests of reference tests/test_inference.py:93-131.
+the allocator tests of reference tests/test_inference.py:93-131, and the dense
+cache test of reference tests/test_inference.py:134-147.
 """
 
 from __future__ import annotations
@@ -11,6 +12,7 @@ from types import SimpleNamespace
 import pytest
 import torch as t
 
+from aiproj_amd.inference.kv_cache import KVCache
 from aiproj_amd.inference.kvcache_config import KVCacheConfig
 from aiproj_amd.inference.page_allocator import CacheCapacityError, PageAllocator, initialize_cache
 from aiproj_amd.inference.paged_kv_cache import PagedKVCache
@@ -218,3 +220,53 @@ def test_rmsnorm_validates_on_the_host_and_refuses_cpu_tensors():
         rmsnorm_forward(t.zeros(2, 4), t.ones(5), 1e-5)
     with pytest.raises(RuntimeError):
         rmsnorm_forward(t.zeros(2, 4), t.ones(4), 1e-5)
+
+
+def test_dense_cache_updates_only_selected_slots():
+    """Reference tests/test_inference.py:134-147 on the host cache."""
+    cache = KVCache(4, 5, 1, 2, t.float32, "cpu")
+    kv = t.arange(6, dtype=t.float32).reshape(3, 1, 2)
+    cache.append_prefill(kv, kv, t.tensor([0, 2, 3]), cache_slots=[3, 1])
+    new = t.full((1, 1, 2), 42.0)
+    cache.append_decode(new, new, cache_slots=[1])
+    assert cache.seq_lens.tolist() == [0, 2, 0, 2]
+    t.testing.assert_close(cache.k_cache[1, 1], new[0])
+    t.testing.assert_close(cache.k_cache[3, :2], kv[:2])
+    with pytest.raises(ValueError):
+        cache.append_decode(new.expand(2, -1, -1), new.expand(2, -1, -1), [1, 1])
+    cache.clear([1])
+    assert cache.seq_lens.tolist() == [0, 0, 0, 2]
+
+
+def test_dense_cache_validation():
+    with pytest.raises(ValueError):
+        KVCache(4, 5, 1, True, t.float32, "cpu")
+    with pytest.raises(ValueError):
+        KVCache(4, 5, 1, 2, t.float8_e4m3fn, "cpu")
+    cache = KVCache(2, 3, 1, 2, t.bfloat16, "cpu")
+    kv = t.ones(2, 1, 2)
+    with pytest.raises(ValueError):
+        cache.append_decode(kv, kv, [[0, 1]])                          # not a vector
+    with pytest.raises(ValueError):
+        cache.append_decode(kv, kv, [0, 2])                            # slot out of range
+    with pytest.raises(ValueError):
+        cache.append_decode(kv, kv, t.tensor([0.0, 1.0]))              # not integer
+    with pytest.raises(ValueError):
+        cache.append_decode(t.ones(2, 1, 3), t.ones(2, 1, 3))          # wrong head size
+    with pytest.raises(ValueError):
+        cache.append_prefill(kv, kv, t.tensor([0, 2]), [0, 1])         # one boundary missing
+    with pytest.raises(ValueError):
+        cache.append_prefill(kv, kv, t.tensor([0, 3, 2]), [0, 1])      # negative length
+    with pytest.raises(ValueError):
+        cache.append_prefill(kv, kv, t.tensor([0.0, 1.0, 2.0]), [0, 1])
+    with pytest.raises(ValueError):
+        cache.append_prefill(t.ones(4, 1, 2), t.ones(4, 1, 2), t.tensor([0, 4, 4]), [0, 1])  # beyond capacity
+    for _ in range(3):
+        cache.append_decode(kv, kv)
+    assert cache.seq_lens.tolist() == [3, 3]
+    with pytest.raises(ValueError):
+        cache.append_decode(kv, kv)                                    # full
+    assert cache.seq_lens.tolist() == [3, 3]
+    assert cache.k_cache.dtype == t.bfloat16 and bool((cache.k_cache == 1).all())
+    empty = cache.slots([])
+    assert empty.dtype == t.long and empty.numel() == 0
