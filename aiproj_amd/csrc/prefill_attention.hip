@@ -746,12 +746,8 @@ prefill_fa_kernel(PrefillArgs a, int32_t units, int32_t upx, int32_t per_xcd) {
         const bool full = kb * kKeys + kKeys - 1 <= qa && kb * kKeys + kKeys <= L;   // wave-uniform
 #pragma unroll
         for (int qt = 0; qt < kFaTiles; ++qt) {
-            // Raw scores (the scale is applied inside the exponent below).
-            float sc_[16];
-#pragma unroll
-            for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-                for (int jj = 0; jj < 4; ++jj) sc_[4 * kt + jj] = sacc[kt][qt][jj];
+            // Raw scores (the scale is applied inside the exponent below), masked in
+            // place so that blocks without a mask keep them in their registers.
             if (!full) {
                 // Keep key kb * 64 + 16 kt + 4 j + jj when it is <= min(row, L - 1).
                 const int lim = min(qa + 16 * qt + m16, L - 1) - (kb * kKeys + 4 * j);
@@ -759,11 +755,11 @@ prefill_fa_kernel(PrefillArgs a, int32_t units, int32_t upx, int32_t per_xcd) {
                 for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
                     for (int jj = 0; jj < 4; ++jj)
-                        sc_[4 * kt + jj] = 16 * kt + jj <= lim ? sc_[4 * kt + jj] : kNegInf;
+                        sacc[kt][qt][jj] = 16 * kt + jj <= lim ? sacc[kt][qt][jj] : kNegInf;
             }
-            float mx = sc_[0];
+            float mx = sacc[0][qt][0];
 #pragma unroll
-            for (int i = 1; i < 16; ++i) mx = fmaxf(mx, sc_[i]);
+            for (int i = 1; i < 16; ++i) mx = fmaxf(mx, sacc[i / 4][qt][i % 4]);
             mx *= a.scale_log2;                        // base-2 units (scale > 0 keeps the order)
             // Lazy rescale: the accumulators keep a reference max m that is only moved
             // when some row's max grows by more than 2^8 (p <= 256 meanwhile, far
@@ -783,7 +779,7 @@ prefill_fa_kernel(PrefillArgs a, int32_t units, int32_t upx, int32_t per_xcd) {
             float pr[16];
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                pr[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc_[i], a.scale_log2, neg_m[qt]));
+                pr[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[i / 4][qt][i % 4], a.scale_log2, neg_m[qt]));
                 l[qt] += pr[i];
             }
 #pragma unroll
