@@ -202,6 +202,14 @@ using namespace kvfp8;
 
 namespace {
 
+// New tokens of a fused append + decode call (kvfp8_append_paged_decode).
+struct NewTokens {
+    const void* k;
+    const void* v;
+    int dtype;
+    int32_t k_sb, v_sb;
+};
+
 struct Plan {
     bool mfma;
     int32_t chunk_tokens;   // generic kernel
@@ -282,12 +290,17 @@ KernelTiming kvfp8::next_kernel_timing() {
 
 namespace {
 
+// Whether a call runs on the MFMA kernel: the plan allows it, the caches are
+// 16-byte aligned, and slot * 32 + count fits the kernel's int32 per sequence.
+bool takes_mfma(const Plan& p, const void* k_cache, const void* v_cache, int64_t bt_rows) {
+    const bool aligned = (((uintptr_t)k_cache | (uintptr_t)v_cache) & 15) == 0;
+    return p.mfma && aligned && bt_rows < ((int64_t)1 << 26);
+}
+
 template <int QT>
 hipError_t dispatch_kv(const DecodeArgs& a, int kv_dtype, const Plan& p, void* workspace, hipStream_t s,
                        int phases) {
-    const bool aligned = (((uintptr_t)a.k_cache | (uintptr_t)a.v_cache) & 15) == 0;
-    // The MFMA kernel keeps slot * 32 + count per sequence in an int32.
-    if (p.mfma && aligned && a.bt_rows < ((int64_t)1 << 26))
+    if (takes_mfma(p, a.k_cache, a.v_cache, a.bt_rows))
         return launch_mfma_decode<QT>(a, kv_dtype, workspace, s, phases);
     if (phases & kPhaseSplit) {
         const int64_t units_total = (int64_t)a.batch * p.max_chunks * a.num_q_heads;
@@ -309,7 +322,8 @@ int paged_decode(const void* q, int q_dtype, int64_t q_stride_b, int64_t q_strid
                  const void* v_cache, int kv_dtype, const float* k_scales, const float* v_scales,
                  int64_t num_blocks, int32_t block_size, const int32_t* block_table, int64_t bt_rows,
                  int64_t bt_width, const void* slots, int slots_dtype, const void* context_lengths, int ctx_dtype,
-                 float sm_scale, void* out, void* workspace, int64_t workspace_bytes, void* stream, int phases);
+                 float sm_scale, void* out, void* workspace, int64_t workspace_bytes, void* stream, int phases,
+                 const NewTokens* fresh);
 
 }  // namespace
 
@@ -338,15 +352,38 @@ extern "C" int64_t kvfp8_decode_workspace_bytes(int32_t batch, int32_t num_q_hea
         slots_dtype, context_lengths, ctx_dtype, sm_scale, out, workspace, workspace_bytes, stream
 
 extern "C" int kvfp8_paged_decode(KVFP8_DECODE_PARAMS) {
-    return paged_decode(KVFP8_DECODE_ARGS, kPhaseSplit | kPhaseReduce);
+    return paged_decode(KVFP8_DECODE_ARGS, kPhaseSplit | kPhaseReduce, nullptr);
 }
 
 extern "C" int kvfp8_paged_decode_split(KVFP8_DECODE_PARAMS) {
-    return paged_decode(KVFP8_DECODE_ARGS, kPhaseSplit);
+    return paged_decode(KVFP8_DECODE_ARGS, kPhaseSplit, nullptr);
 }
 
 extern "C" int kvfp8_paged_decode_reduce(KVFP8_DECODE_PARAMS) {
-    return paged_decode(KVFP8_DECODE_ARGS, kPhaseReduce);
+    return paged_decode(KVFP8_DECODE_ARGS, kPhaseReduce, nullptr);
+}
+
+extern "C" int kvfp8_append_decode_supported(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+                                             int32_t head_dim, int64_t bt_rows, int64_t bt_width,
+                                             int32_t block_size, int kv_dtype) {
+    if (kv_dtype != KVFP8_E4M3FN || batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || bt_rows <= 0 ||
+        bt_width <= 0 || !pow2(block_size) || num_q_heads % num_kv_heads != 0)
+        return 0;
+    const Plan p = make_plan(batch, num_q_heads, num_kv_heads, head_dim, bt_width, block_size, kv_dtype);
+    return p.mfma && bt_rows < ((int64_t)1 << 26) ? 1 : 0;
+}
+
+extern "C" int kvfp8_append_paged_decode(KVFP8_DECODE_PARAMS, const void* k_new, const void* v_new, int new_dtype,
+                                         int64_t k_new_stride_b, int64_t k_new_stride_h, int64_t v_new_stride_b,
+                                         int64_t v_new_stride_h) {
+    if (new_dtype != KVFP8_F32 && new_dtype != KVFP8_F16 && new_dtype != KVFP8_BF16) return KVFP8_EDTYPE;
+    if (batch > 0 && (!k_new || !v_new)) return KVFP8_ENULL;
+    // Heads are contiguous within a row; row strides are int32 element counts.
+    if (k_new_stride_h != head_dim || v_new_stride_h != head_dim || k_new_stride_b < 0 || v_new_stride_b < 0 ||
+        k_new_stride_b > INT32_MAX || v_new_stride_b > INT32_MAX)
+        return KVFP8_ESTRIDE;
+    const NewTokens fresh{k_new, v_new, new_dtype, (int32_t)k_new_stride_b, (int32_t)v_new_stride_b};
+    return paged_decode(KVFP8_DECODE_ARGS, kPhaseSplit | kPhaseReduce, &fresh);
 }
 
 namespace {
@@ -356,7 +393,8 @@ int paged_decode(const void* q, int q_dtype, int64_t q_stride_b, int64_t q_strid
                  const void* v_cache, int kv_dtype, const float* k_scales, const float* v_scales,
                  int64_t num_blocks, int32_t block_size, const int32_t* block_table, int64_t bt_rows,
                  int64_t bt_width, const void* slots, int slots_dtype, const void* context_lengths, int ctx_dtype,
-                 float sm_scale, void* out, void* workspace, int64_t workspace_bytes, void* stream, int phases) {
+                 float sm_scale, void* out, void* workspace, int64_t workspace_bytes, void* stream, int phases,
+                 const NewTokens* fresh) {
     if (q_dtype != KVFP8_F32 && q_dtype != KVFP8_F16 && q_dtype != KVFP8_BF16) return KVFP8_EDTYPE;
     if (kv_dtype != KVFP8_E4M3FN && kv_dtype != KVFP8_BF16 && kv_dtype != KVFP8_F16 && kv_dtype != KVFP8_F32)
         return KVFP8_EDTYPE;
@@ -373,6 +411,8 @@ int paged_decode(const void* q, int q_dtype, int64_t q_stride_b, int64_t q_strid
     const Plan p = make_plan(batch, num_q_heads, num_kv_heads, head_dim, bt_width, block_size, kv_dtype);
     const int64_t need = workspace_for(p, batch, num_q_heads, num_kv_heads, head_dim);
     if (!workspace || workspace_bytes < need) return KVFP8_EWORKSPACE;
+    // The fused append runs inside the MFMA kernel over an e4m3fn cache only.
+    if (fresh && (kv_dtype != KVFP8_E4M3FN || !takes_mfma(p, k_cache, v_cache, bt_rows))) return KVFP8_ESHAPE;
 
     const int64_t states = (int64_t)batch * p.max_chunks * num_q_heads;
     char* ws = reinterpret_cast<char*>(workspace);
@@ -405,6 +445,11 @@ int paged_decode(const void* q, int q_dtype, int64_t q_stride_b, int64_t q_strid
     a.part_acc = reinterpret_cast<float*>(ws + 2 * align256(states * sizeof(float)));
     a.chunk_tokens = p.chunk_tokens;
     a.max_chunks = p.max_chunks;
+    a.new_k = fresh ? fresh->k : nullptr;
+    a.new_v = fresh ? fresh->v : nullptr;
+    a.new_dtype = fresh ? fresh->dtype : KVFP8_BF16;
+    a.new_k_sb = fresh ? fresh->k_sb : 0;
+    a.new_v_sb = fresh ? fresh->v_sb : 0;
 
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     hipError_t err;

@@ -43,6 +43,14 @@ struct DecodeArgs {
     float* part_acc;
     int32_t chunk_tokens;     // tokens per work item (a multiple of 16)
     int32_t max_chunks;       // ceil(bt_width * block_size / chunk_tokens)
+    // Fused append (kvfp8_append_paged_decode): the new token of every sequence,
+    // rows [batch, Hkv, D] with element strides (row stride, D, 1), quantized into
+    // the cache at position context_lengths[b] - 1 before it is attended. Read only
+    // by the kernels built for the fused call.
+    const void* new_k;
+    const void* new_v;
+    int32_t new_dtype;
+    int32_t new_k_sb, new_v_sb;
 };
 
 __device__ __forceinline__ int64_t load_i(const void* p, int is64, int64_t i) {

@@ -562,7 +562,89 @@ __device__ __forceinline__ void compute_step(WaveState<C>& st, const StepData<C,
     }
 }
 
-template <int C, int QT, int ES, int kSets>
+// Fused append of one sequence's new token for KV head h, by the wave that serves
+// h in the workgroup attending over the sequence's last tile: the same rule and
+// arithmetic as quantize_append_kernel (amax as an integer max of |x| bits, which
+// propagates NaN; scale = amax / 448 by IEEE division, 1 when amax is 0 or NaN;
+// codes from the corrected reciprocal on finite rows, else clamp and encode).
+// Lane l holds elements C l .. C l + C - 1. fetch() issues the loads and put()
+// quantizes and stores; the wave's own loads of that page row come after put()
+// in its instruction order, which the memory pipeline keeps for one wave, so
+// they read the new codes and scales.
+template <int C>
+struct NewRow {
+    float k[C], v[C];
+    int64_t row;      // cache row (page slot * Hkv + h), or -1: no write
+};
+
+typedef const __attribute__((address_space(4))) int64_t* const_i64_ptr;
+
+template <int C>
+__device__ __forceinline__ void fetch_new_token(const MfmaArgs& a, int b, int h, const int32_t* table_row,
+                                                int64_t len, int lane, NewRow<C>& r) {
+    constexpr int D = 64 * C;
+    r.row = -1;
+    // Only where the length was not clipped to the table (scalar loads: their wait
+    // does not cover the vector loads in flight).
+    const int64_t caddr = uniform64((int64_t)(uintptr_t)a.d.ctx);
+    const int64_t ctx = a.d.ctx64 ? ((const_i64_ptr)(uintptr_t)caddr)[b] : (int64_t)((const_i32_ptr)(uintptr_t)caddr)[b];
+    if (ctx != len) return;
+    const int64_t pos = len - 1;
+    const int64_t addr = uniform64((int64_t)(uintptr_t)(table_row + (pos >> a.d.bs_shift)));
+    const int64_t page = *(const_i32_ptr)(uintptr_t)addr;
+    if (page < 0 || page >= a.d.num_blocks) return;           // the reads skip this page too
+    r.row = ((page << a.d.bs_shift) + (pos & (a.d.block_size - 1))) * a.d.num_kv_heads + h;
+    // The new-row fields are read from the kernel-argument segment here, where they
+    // are used: the empty asm keeps the compiler from hoisting these loads to the
+    // kernel's entry and holding them in scalar registers through the step loop.
+    const char* kargs = reinterpret_cast<const char*>(__builtin_amdgcn_kernarg_segment_ptr());
+    __asm__ volatile("" : "+s"(kargs));
+    typedef const __attribute__((address_space(4))) DecodeArgs* const_args_ptr;
+    const_args_ptr na = (const_args_ptr)(kargs + offsetof(MfmaArgs, d));
+    const int dtype = na->new_dtype;
+#pragma unroll
+    for (int kv = 0; kv < 2; ++kv) {
+        const int64_t off = (int64_t)b * (kv ? na->new_v_sb : na->new_k_sb) + (int64_t)h * D + C * lane;
+        const void* src = kv ? na->new_v : na->new_k;
+        float* x = kv ? r.v : r.k;
+#pragma unroll
+        for (int e = 0; e < C; ++e)
+            x[e] = dtype == KVFP8_F32 ? reinterpret_cast<const float*>(src)[off + e]
+                 : dtype == KVFP8_F16 ? f16_to_f32(reinterpret_cast<const uint16_t*>(src)[off + e])
+                                      : bf16_to_f32(reinterpret_cast<const uint16_t*>(src)[off + e]);
+    }
+}
+
+template <int C>
+__device__ __forceinline__ void put_new_token(const MfmaArgs& a, const NewRow<C>& r, int lane) {
+    constexpr int D = 64 * C;
+    if (r.row < 0) return;
+#pragma unroll
+    for (int kv = 0; kv < 2; ++kv) {
+        const float* x = kv ? r.v : r.k;
+        uint32_t amax = abs_bits(x[0]);
+#pragma unroll
+        for (int e = 1; e < C; ++e) amax = max(amax, abs_bits(x[e]));
+#pragma unroll
+        for (int s = 1; s < 64; s <<= 1) amax = max(amax, (uint32_t)__shfl_xor((int)amax, s));
+        const float scale = row_scale(amax);
+        const RowDivider div(scale);
+        uint32_t codes;
+        if (div.fast && amax < 0x7F800000u) {
+            codes = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(div.corrected(x[0]), C > 1 ? div.corrected(x[C - 1]) : 0.0f,
+                                                              0, false);
+        } else {
+            codes = clamp_encode(x[0] / scale);
+            if constexpr (C > 1) codes |= (uint32_t)clamp_encode(x[C - 1] / scale) << 8;
+        }
+        uint8_t* dst = reinterpret_cast<uint8_t*>(const_cast<void*>(kv ? a.d.v_cache : a.d.k_cache)) + r.row * D + C * lane;
+        if constexpr (C == 2) *reinterpret_cast<uint16_t*>(dst) = (uint16_t)codes;
+        else *dst = (uint8_t)codes;
+        if (lane == 0) const_cast<float*>(kv ? a.d.v_scales : a.d.k_scales)[r.row] = scale;
+    }
+}
+
+template <int C, int QT, int ES, int kSets, bool kAppend>
 __global__ void __launch_bounds__(kMaxThreads)
 decode_mfma_kernel(MfmaArgs a) {
     constexpr int D = 64 * C;
@@ -630,6 +712,19 @@ decode_mfma_kernel(MfmaArgs a) {
             const int64_t slot = mt >> 5;
             const int64_t len = 16 * (int64_t)(seq1 - seq0 - 1) + (mt & 31);
             const int32_t* table_row = a.d.block_table + slot * a.d.bt_width;
+            // This workgroup attends over the sequence's last tile: it writes the
+            // sequence's new token. Its loads go out first; the quantized row is
+            // stored before the loads of the tile that holds it (after the first
+            // issued steps when that tile is not among them).
+            const bool append = kAppend && seg1 == seq1;
+            NewRow<C> fresh;
+            if constexpr (kAppend) {
+                if (append) fetch_new_token<C>(a, b, h, table_row, len, lane, fresh);
+            }
+            const bool put_early = t1 - 1 < t0 + (ES == 1 ? 4 : 2);
+            if constexpr (kAppend) {
+                if (append && put_early) put_new_token<C>(a, fresh, lane);
+            }
 
             WaveState<C> st;
 #pragma unroll
@@ -660,6 +755,9 @@ decode_mfma_kernel(MfmaArgs a) {
             issue(buf0, T, r0a, r0b);
             if constexpr (ES == 1) {
                 if (T + 2 < t1) issue(buf1, T + 2, r1a, r1b);
+            }
+            if constexpr (kAppend) {
+                if (append && !put_early) put_new_token<C>(a, fresh, lane);
             }
             bf16x8_t qh[2 * C], ql[2 * C];
             q_operands<C, ES, QT, kQOps, kHiLo>(qraw, G, lane, qh, ql);
@@ -848,7 +946,7 @@ int64_t max_groups(int32_t num_kv_heads) {
     return (int64_t)device_cus() * (per_cu > 0 ? per_cu : 1);
 }
 
-template <int C, int QT, int ES, int kSets>
+template <int C, int QT, int ES, int kSets, bool kAppend = false>
 hipError_t launch_c(const MfmaArgs& a, int64_t cap, hipStream_t s, int phases) {
     const int threads = 64 * waves_for(a.d.num_kv_heads);
     const size_t lds = (size_t)(2 * a.d.batch + 1) * sizeof(int32_t);
@@ -862,7 +960,7 @@ hipError_t launch_c(const MfmaArgs& a, int64_t cap, hipStream_t s, int phases) {
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
     int& per_cu = resident[dev][threads / 64];
     if (per_cu == 0) {
-        const void* fn = reinterpret_cast<const void*>(&decode_mfma_kernel<C, QT, ES, kSets>);
+        const void* fn = reinterpret_cast<const void*>(&decode_mfma_kernel<C, QT, ES, kSets, kAppend>);
         int n = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, threads, 0) != hipSuccess || n <= 0) n = 1;
         per_cu = n;
@@ -878,7 +976,7 @@ hipError_t launch_c(const MfmaArgs& a, int64_t cap, hipStream_t s, int phases) {
     int64_t groups = (int64_t)device_cus() * (fit > 0 ? fit : 1);
     groups = groups < cap ? groups : cap;
     if (phases & kPhaseSplit) {
-        const hipError_t err = launch_timed(decode_mfma_kernel<C, QT, ES, kSets>, dim3((unsigned)groups), dim3(threads),
+        const hipError_t err = launch_timed(decode_mfma_kernel<C, QT, ES, kSets, kAppend>, dim3((unsigned)groups), dim3(threads),
                                             lds, s, next_kernel_timing(), a);
         if (err != hipSuccess) return err;
     }
@@ -942,6 +1040,12 @@ hipError_t launch_mfma_decode(const DecodeArgs& d, int kv_dtype, void* workspace
     if (kv_dtype == KVFP8_BF16)
         return d.head_dim == 64 ? launch_c<1, QT, 2, 1>(a, cap, stream, phases)
                                 : launch_c<2, QT, 2, 1>(a, cap, stream, phases);
+    if (d.new_k != nullptr) {
+        // Fused append + decode (e4m3fn only; the caller checked the shape).
+        if (d.head_dim == 64) return launch_c<1, QT, 1, 1, true>(a, cap, stream, phases);
+        return d.num_q_heads / d.num_kv_heads > 8 ? launch_c<2, QT, 1, 2, true>(a, cap, stream, phases)
+                                                   : launch_c<2, QT, 1, 1, true>(a, cap, stream, phases);
+    }
     if (d.head_dim == 64) return launch_c<1, QT, 1, 1>(a, cap, stream, phases);
     // Whole-row K layout: q heads 8..15 of a group need the second QK set.
     return d.num_q_heads / d.num_kv_heads > 8 ? launch_c<2, QT, 1, 2>(a, cap, stream, phases)

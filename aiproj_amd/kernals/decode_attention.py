@@ -16,6 +16,12 @@ plan is built on the device inside the kernel (reference `:87-103` reads
 The work is two launches through the C ABI `kvfp8_paged_decode` (include/kvfp8.h);
 `prepare_decode` returns the prepared call so the two launches can also be enqueued
 one at a time.
+
+`append_decode_attention(q, ks, vs, paged_kv_cache, cache_batch_context)` is the
+decode step's append and attention together (reference `model/attention.py:86-99`
+makes the two calls back to back). On an FP8 cache the decode kernel itself writes
+each sequence's new token (`kvfp8_append_paged_decode`), so the step has no
+separate append launch; other caches and shapes make the two calls.
 """
 
 from __future__ import annotations
@@ -157,3 +163,45 @@ def prepare_decode(q, paged_kv_cache, cache_batch_context=None) -> DecodeCall:
     )
     keep = (q, k_cache, v_cache, k_scales, v_scales, block_table, cache_slots, context_lengths)
     return DecodeCall(output, workspace, args, keep)
+
+
+def append_decode_attention(q, ks, vs, paged_kv_cache, cache_batch_context):
+    """`paged_kv_cache.append_kv(ctx.physical_blocks, ctx.block_offsets, ks, vs)` followed by
+    `decode_attention_wrapper(q, paged_kv_cache, ctx)`, the decode step of reference
+    `model/attention.py:86-99`, with the same results (cache codes and scales bit-identical).
+
+    ks, vs: [B, Hkv, D], the new token of every sequence of the batch. The fused form
+    writes the new token of sequence b at its last attended position, context_lengths[b] - 1
+    through the block table, which is where a decode step's write locations point
+    (`PageAllocator.resolve_batch_locations`: the position of the new token is the
+    committed length, and the context length is that plus one); it is taken on e4m3fn
+    caches whose shapes the MFMA kernel handles, and the two calls are made otherwise.
+    """
+    cache, ctx = paged_kv_cache, cache_batch_context
+    b, hq, d = q.shape
+    hkv = cache.k.shape[2]
+    expected = (b, hkv, d)
+    if ks.shape != expected or vs.shape != expected:
+        raise ValueError(f"append_decode_attention: new K/V must be {expected}")
+    fused = (cache.quantized and ks.dtype in _Q_DTYPES and q.device.type == "cuda"
+             and _native.lib().kvfp8_append_decode_supported(
+                 b, hq, hkv, d, ctx.block_table.shape[0], ctx.block_table.shape[1], cache.block_size,
+                 _native.dtype_code(cache.k.dtype)) == 1)
+    if not fused:
+        cache.append_kv(ctx.physical_blocks, ctx.block_offsets, ks, vs)
+        return decode_attention_wrapper(q, cache, ctx)
+    _native.require_gpu(ks, vs, cache.k, what="append_decode_attention")
+    call = prepare_decode(q, cache, ctx)
+    if call.args is None:
+        return call.output
+    if vs.dtype != ks.dtype:
+        vs = vs.to(ks.dtype)
+    if ks.stride(2) != 1 or ks.stride(1) != d:
+        ks = ks.contiguous()
+    if vs.stride(2) != 1 or vs.stride(1) != d:
+        vs = vs.contiguous()
+    rc = _native.lib().kvfp8_append_paged_decode(
+        *call.args, ks.data_ptr(), vs.data_ptr(), _native.dtype_code(ks.dtype),
+        ks.stride(0), ks.stride(1), vs.stride(0), vs.stride(1))
+    _native.check(rc, "kvfp8_append_paged_decode")
+    return call.output

@@ -18,7 +18,8 @@ dense SwiGLU, which is that MoE with one expert and top-1 routing (routing weigh
 1.0). It is written here as `down(silu(gate(x)) * up(x))`.
 
 What runs where: the norms (`rmsnorm_kernel`, residual add fused into the next
-norm), the cache write and the decode attention are this library's HIP kernels;
+norm), the cache write and the decode attention are this library's HIP kernels (in
+decode, the new token's quantized write is done by the decode kernel itself);
 the projections and the FFN are plain GEMMs (hipBLASLt through torch); prompt
 (prefill) attention is the varlen causal HIP kernel behind `flash_attention_forward`,
 as the reference calls its FlashAttentionFunction there (`attention.py:103-110`).
@@ -33,7 +34,7 @@ import torch as t
 from torch import nn
 from torch.nn import functional as F
 
-from aiproj_amd.kernals.decode_attention import decode_attention_wrapper
+from aiproj_amd.kernals.decode_attention import append_decode_attention
 from aiproj_amd.kernals.flash_attention import flash_attention_forward
 from aiproj_amd.model.rmsnorm import add_rmsnorm, rmsnorm_forward
 
@@ -128,8 +129,9 @@ class Attention(nn.Module):
                                              meta.max_seqlen, 1.0 / math.sqrt(cfg.head_dim))
             cache.append_kv(ctx.physical_blocks, ctx.block_offsets, k, v)
         else:
-            cache.append_kv(ctx.physical_blocks, ctx.block_offsets, k, v)
-            out = decode_attention_wrapper(q, cache, ctx)
+            # append_kv + decode_attention_wrapper (`attention.py:86-99`) as one call: on the
+            # FP8 cache the decode kernel writes each sequence's new token itself.
+            out = append_decode_attention(q, k, v, cache, ctx)
         return self.o_proj(out.reshape(-1, self.q_dim))
 
 

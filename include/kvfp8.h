@@ -209,6 +209,45 @@ int kvfp8_prefill_attention(const void* q_dev, const void* k_dev, const void* v_
                             float scale, void* out_dev, float* lse_dev, void* stream);
 
 /*
+ * Fused append + decode: the quantize-and-scatter write of every sequence's new
+ * token and the paged decode attention over the context that includes it, in the
+ * decode kernel's launches (no separate append launch).
+ *
+ * Replaces the two calls the reference makes back to back in its decode step,
+ * reference src/torch_llm/model/attention.py:86-99 (PagedKVCache.append_kv, then
+ * decode_attention_wrapper), for the case where the new token of sequence b is
+ * its last attended position: it is written at position context_lengths[b] - 1,
+ * page block_table[slots[b], (context_lengths[b] - 1) / block_size], with the
+ * kvfp8_quantize_append rule (codes and scales bit-identical to it), before the
+ * attention reads it. A sequence whose length is 0, is clipped to the table
+ * width, or whose last page is outside [0, num_blocks) gets no write.
+ *
+ * Takes the kvfp8_paged_decode arguments, then the new rows: k_new/v_new
+ * [batch, H_kv, D] (f32/f16/bf16) with element strides (stride_b, stride_h, 1),
+ * stride_h == D and stride_b below 2^31. e4m3fn caches on the MFMA kernel only:
+ * other shapes return KVFP8_ESHAPE before launching anything
+ * (kvfp8_append_decode_supported says which).
+ */
+int kvfp8_append_paged_decode(const void* q_dev, int q_dtype, int64_t q_stride_b, int64_t q_stride_h,
+                              int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                              const void* k_cache_dev, const void* v_cache_dev, int kv_dtype,
+                              const float* k_scales_dev, const float* v_scales_dev,
+                              int64_t num_blocks, int32_t block_size,
+                              const int32_t* block_table_dev, int64_t bt_rows, int64_t bt_width,
+                              const void* slots_dev, int slots_dtype,
+                              const void* context_lengths_dev, int ctx_dtype,
+                              float sm_scale, void* out_dev,
+                              void* workspace_dev, int64_t workspace_bytes, void* stream,
+                              const void* k_new_dev, const void* v_new_dev, int new_dtype,
+                              int64_t k_new_stride_b, int64_t k_new_stride_h,
+                              int64_t v_new_stride_b, int64_t v_new_stride_h);
+
+/* 1 when kvfp8_append_paged_decode handles these shapes (e4m3fn cache on the MFMA
+ * kernel), else 0. Shapes only; pointer alignment is checked by the call. */
+int kvfp8_append_decode_supported(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                  int64_t bt_rows, int64_t bt_width, int32_t block_size, int kv_dtype);
+
+/*
  * Interleaved-pair rotary embedding in place on heads [0, heads) of every row of x
  * (element strides row_stride, head_stride; pairs (2i, 2i+1) of head_dim):
  *   x0' = c x0 - s x1, x1' = s x0 + c x1,  c/s = cos/sin_table[positions[r], i]
