@@ -49,6 +49,7 @@ SIGNATURES = {
     "kvfp8_add_rmsnorm_forward": (_INT, [_P, _P, _INT, _I64, _I64, _I64, _I32, _P, _INT, ctypes.c_float,
                                          _P, _I64, _P, _I64, _P, _P]),
     "kvfp8_rope_inplace": (_INT, [_P, _INT, _I64, _I32, _I32, _I64, _I64, _P, _INT, _P, _P, _INT, _I64, _P]),
+    "kvfp8_silu_mul": (_INT, [_P, _INT, _I64, _I32, _I64, _P, _I64, _P]),
     "kvfp8_prefill_attention": (_INT, [_P, _P, _P, _INT, _I64, _I32, _I32, _I32, _P, _INT, _I32, _I32,
                                        ctypes.c_float, _P, _P, _P]),
     "kvfp8_timing_enable": (_INT, [_I32]),

@@ -597,10 +597,10 @@ __device__ __forceinline__ void fetch_new_token(const MfmaArgs& a, int b, int h,
     // The new-row fields are read from the kernel-argument segment here, where they
     // are used: the empty asm keeps the compiler from hoisting these loads to the
     // kernel's entry and holding them in scalar registers through the step loop.
-    const char* kargs = reinterpret_cast<const char*>(__builtin_amdgcn_kernarg_segment_ptr());
+    uint64_t kargs = (uint64_t)(uintptr_t)__builtin_amdgcn_kernarg_segment_ptr();
     __asm__ volatile("" : "+s"(kargs));
     typedef const __attribute__((address_space(4))) DecodeArgs* const_args_ptr;
-    const_args_ptr na = (const_args_ptr)(kargs + offsetof(MfmaArgs, d));
+    const_args_ptr na = (const_args_ptr)(uintptr_t)(kargs + offsetof(MfmaArgs, d));
     const int dtype = na->new_dtype;
 #pragma unroll
     for (int kv = 0; kv < 2; ++kv) {

@@ -15,11 +15,13 @@ the prompt and then appends them to the cache; decode appends the new token's K/
 
 The reference's only FFN is a top-k MoE (`model/moe/moe.py`); config 5 asks for a
 dense SwiGLU, which is that MoE with one expert and top-1 routing (routing weight
-1.0). It is written here as `down(silu(gate(x)) * up(x))`.
+1.0). It is written here as `down(silu(gate(x)) * up(x))`, the activation in float32
+with one rounding as in the reference's fused SwiGLU kernel.
 
 What runs where: the norms (`rmsnorm_kernel`, residual add fused into the next
-norm), the cache write and the decode attention are this library's HIP kernels (in
-decode, the new token's quantized write is done by the decode kernel itself);
+norm), RoPE, the SwiGLU activation, the cache write and the decode attention are this
+library's HIP kernels (in decode, the new token's quantized write is done by the decode
+kernel itself);
 the projections and the FFN are plain GEMMs (hipBLASLt through torch); prompt
 (prefill) attention is the varlen causal HIP kernel behind `flash_attention_forward`,
 as the reference calls its FlashAttentionFunction there (`attention.py:103-110`).
@@ -135,6 +137,22 @@ class Attention(nn.Module):
         return self.o_proj(out.reshape(-1, self.q_dim))
 
 
+def silu_mul(gu: t.Tensor, d_ff: int) -> t.Tensor:
+    """silu(gu[:, :d_ff]) * gu[:, d_ff:] in float32 with one rounding, as the reference's
+    fused SwiGLU computes it (`kernals/moe/grouped_swiglu_up.py:239`): one launch of the
+    HIP kernel `silu_mul_kernel` (C ABI `kvfp8_silu_mul`)."""
+    from aiproj_amd import _native
+
+    device = _native.require_gpu(gu, what="silu_mul")
+    if gu.ndim != 2 or gu.shape[1] != 2 * d_ff or gu.stride(1) != 1:
+        raise ValueError("silu_mul: rows of gate then up, unit element stride")
+    out = t.empty((gu.shape[0], d_ff), dtype=gu.dtype, device=gu.device)
+    rc = _native.lib().kvfp8_silu_mul(gu.data_ptr(), _native.dtype_code(gu.dtype), gu.shape[0], d_ff, gu.stride(0),
+                                      out.data_ptr(), out.stride(0), _native.stream_handle(device))
+    _native.check(rc, "kvfp8_silu_mul")
+    return out
+
+
 class SwiGLU(nn.Module):
     def __init__(self, cfg: ModelConfig):
         super().__init__()
@@ -143,8 +161,7 @@ class SwiGLU(nn.Module):
         self.down = nn.Linear(cfg.d_ff, cfg.d_model, bias=False)
 
     def forward(self, h: t.Tensor) -> t.Tensor:
-        gu = self.gate_up(h)
-        return self.down(F.silu(gu[:, :self.d_ff]) * gu[:, self.d_ff:])
+        return self.down(silu_mul(self.gate_up(h), self.d_ff))
 
 
 class DecoderLayer(nn.Module):

@@ -263,6 +263,17 @@ int kvfp8_rope_inplace(void* x_dev, int dtype, int64_t rows, int32_t heads, int3
                        int64_t table_rows, void* stream);
 
 /*
+ * SwiGLU activation: out[r, j] = silu(g) * u with g = x[r, j], u = x[r, n + j] and
+ * silu(g) = g * (1 / (1 + exp(-g))), in float32 with one rounding to the dtype
+ * (f32/f16/bf16). x rows hold gate then up (row stride >= 2 n elements); out rows
+ * n elements (row stride >= n).
+ * Replaces the activation of reference src/torch_llm/kernals/moe/grouped_swiglu_up.py:239
+ * (applied there to the float32 accumulators of the fused gate/up product).
+ */
+int kvfp8_silu_mul(const void* x_dev, int dtype, int64_t rows, int32_t n, int64_t x_row_stride,
+                   void* out_dev, int64_t out_row_stride, void* stream);
+
+/*
  * Kernel timing hook for benchmarks (not part of the reference interface).
  * kvfp8_timing_enable(n) arms start/stop HIP events on the dispatch packets of
  * the next n decode-kernel launches (hipExtLaunchKernel, on the stream each launch

@@ -112,3 +112,23 @@ def test_rope_kernel_is_bit_identical_to_the_reference_op_sequence(dtype, table_
     want[ok, :5] = rope(want[ok, :5], pos[ok])
     got = rope.apply_(x.clone(), pos, heads=5).view(50, 7, 64)
     assert t.equal(got, want)
+
+
+@t.inference_mode()
+@pytest.mark.parametrize("dtype", [t.bfloat16, t.float16, t.float32])
+@pytest.mark.parametrize("rows,d_ff,pad", [(64, 5632, 0), (5, 37, 0), (7, 64, 3), (1, 8, 8)])
+def test_silu_mul_kernel_against_float64(dtype, rows, d_ff, pad):
+    """silu(gate) * up from the fused projection rows, one rounding: within one unit in
+    the last place of the float64 value (16-byte path and element path, strided rows)."""
+    from aiproj_amd.model.transformer import silu_mul
+
+    g = t.Generator(device="cuda").manual_seed(rows * 7 + d_ff)
+    wide = (t.randn(rows, 2 * d_ff + pad, device="cuda", generator=g) * 4).to(dtype)
+    gu = wide[:, :2 * d_ff]
+    out = silu_mul(gu, d_ff)
+    x = gu.double().cpu()
+    want = x[:, :d_ff] * t.sigmoid(x[:, :d_ff]) * x[:, d_ff:]
+    ulp = {t.bfloat16: 2.0 ** -7, t.float16: 2.0 ** -10, t.float32: 2.0 ** -22}[dtype]
+    t.testing.assert_close(out.double().cpu(), want, rtol=ulp, atol=1e-30 if dtype == t.float32 else 1e-6)
+    with pytest.raises(ValueError):
+        silu_mul(gu[:, :-1], d_ff)
