@@ -141,3 +141,23 @@ def test_support_query_and_argument_checks():
     k, v = workloads.new_kv(w, "cuda", 0)
     with pytest.raises(ValueError):
         append_decode_attention(w.q, k[:1], v[:1], fused, ctx)
+
+
+@t.inference_mode()
+@pytest.mark.parametrize("q_dtype", [t.float32, t.float16])
+@pytest.mark.parametrize("index_dtype", [t.int32, t.int64])
+def test_fused_step_query_and_index_dtypes(q_dtype, index_dtype):
+    """f32 / f16 queries (the kernel's hi + lo query operands) and int32 / int64 context
+    lengths and slots (the owning wave reads the length itself)."""
+    spec = workloads.spec("cfg2", lengths=[3, 17, 250, 1000, 64])
+    w, ctx, separate, fused = caches_for(spec)
+    ctx = CacheContainer(ctx.cache_slots.to(index_dtype), ctx.physical_blocks, ctx.block_offsets,
+                         ctx.context_lengths.to(index_dtype), ctx.block_table)
+    q = w.q.to(q_dtype)
+    k, v = workloads.new_kv(w, "cuda", 1)
+    separate.append_kv(w.new_blocks, w.new_offsets, k, v)
+    want = decode_attention_wrapper(q, separate, ctx)
+    got = append_decode_attention(q, k, v, fused, ctx)
+    t.cuda.synchronize()
+    assert_same(separate, fused)
+    assert got.dtype == q_dtype and t.equal(got, want)
