@@ -819,19 +819,16 @@ decode_mfma_kernel(MfmaArgs a) {
                             store_out<QT>(a.d, b, hq, NB * (4 * j + jj) + nb, lt > 0.0f ? st.o[nb][jj] * inv : 0.0f);
                     }
                 } else {
-                    // Partial states go out as nontemporal stores: the combine kernel reads
-                    // them once, and the end-of-kernel release has fewer dirty L2 lines to
-                    // write back (about 0.6 us per north-star step, measured A/B).
                     const int64_t pi = (int64_t)slot_index * a.d.num_q_heads + hq;
                     float* acc = a.part_acc + pi * D;
 #pragma unroll
                     for (int jj = 0; jj < 4; ++jj) {
 #pragma unroll
-                        for (int nb = 0; nb < NB; ++nb) __builtin_nontemporal_store(st.o[nb][jj], &acc[NB * (4 * j + jj) + nb]);
+                        for (int nb = 0; nb < NB; ++nb) acc[NB * (4 * j + jj) + nb] = st.o[nb][jj];
                     }
                     if (j == 0) {
-                        __builtin_nontemporal_store(st.m, &a.part_m[pi]);
-                        __builtin_nontemporal_store(lt, &a.part_l[pi]);
+                        a.part_m[pi] = st.m;
+                        a.part_l[pi] = lt;
                     }
                 }
             }
