@@ -837,6 +837,21 @@ decode_mfma_kernel(MfmaArgs a) {
     }
 }
 
+// Four consecutive output elements d0 .. d0 + 3 (d0 a multiple of 4) as one store.
+template <int QT>
+__device__ __forceinline__ void store_out4(const DecodeArgs& a, int b, int hq, int d0, float x0, float x1, float x2,
+                                           float x3) {
+    using T = typename Elem<QT>::T;
+    T* dst = reinterpret_cast<T*>(a.out) + ((int64_t)b * a.num_q_heads + hq) * a.head_dim + d0;
+    if constexpr (QT == KVFP8_F32) {
+        *reinterpret_cast<float4*>(dst) = make_float4(x0, x1, x2, x3);
+    } else {
+        const uint32_t lo = (uint32_t)Elem<QT>::store(x0) | ((uint32_t)Elem<QT>::store(x1) << 16);
+        const uint32_t hi = (uint32_t)Elem<QT>::store(x2) | ((uint32_t)Elem<QT>::store(x3) << 16);
+        *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
+    }
+}
+
 // Workgroup whose tile range holds tile x: the largest w with w W / groups <= x.
 __device__ __forceinline__ int32_t group_of(int64_t x, int64_t total, int64_t groups) {
     return (int32_t)(((x + 1) * groups - 1) / total);
@@ -854,7 +869,9 @@ combine_mfma_kernel(MfmaArgs a) {
     constexpr int D = 64 * C;
     constexpr int kLanesPerPiece = D / 4;
     constexpr int kPiecesPerPass = 64 / kLanesPerPiece;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    // The wave index as a scalar, so that the per-sequence plan entries below are
+    // scalar loads.
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int64_t pair = (int64_t)blockIdx.x * 4 + wave;
     if (pair >= (int64_t)a.d.batch * a.d.num_q_heads) return;
     const int b = (int)(pair / a.d.num_q_heads);
@@ -862,10 +879,7 @@ combine_mfma_kernel(MfmaArgs a) {
     const int32_t t0 = a.plan[b], t1 = a.plan[b + 1];
     const int d4 = lane % kLanesPerPiece, po = lane / kLanesPerPiece;
     if (t1 == t0) {
-        if (po == 0) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) store_out<QT>(a.d, b, hq, 4 * d4 + e, 0.0f);
-        }
+        if (po == 0) store_out4<QT>(a.d, b, hq, 4 * d4, 0.0f, 0.0f, 0.0f, 0.0f);
         return;
     }
     const int64_t total = a.plan[a.d.batch];
@@ -915,10 +929,8 @@ combine_mfma_kernel(MfmaArgs a) {
     }
     if (po == 0) {
         const bool ok = den > 0.0f;
-        store_out<QT>(a.d, b, hq, 4 * d4 + 0, ok ? num.x / den : 0.0f);
-        store_out<QT>(a.d, b, hq, 4 * d4 + 1, ok ? num.y / den : 0.0f);
-        store_out<QT>(a.d, b, hq, 4 * d4 + 2, ok ? num.z / den : 0.0f);
-        store_out<QT>(a.d, b, hq, 4 * d4 + 3, ok ? num.w / den : 0.0f);
+        store_out4<QT>(a.d, b, hq, 4 * d4, ok ? num.x / den : 0.0f, ok ? num.y / den : 0.0f,
+                       ok ? num.z / den : 0.0f, ok ? num.w / den : 0.0f);
     }
 }
 
