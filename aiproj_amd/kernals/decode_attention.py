@@ -26,6 +26,7 @@ separate append launch; other caches and shapes make the two calls.
 
 from __future__ import annotations
 
+import functools
 import math
 from dataclasses import dataclass
 
@@ -165,6 +166,12 @@ def prepare_decode(q, paged_kv_cache, cache_batch_context=None) -> DecodeCall:
     return DecodeCall(output, workspace, args, keep)
 
 
+@functools.lru_cache(maxsize=256)
+def _fused_supported(b, hq, hkv, d, bt_rows, bt_width, block_size, kv_code) -> bool:
+    """kvfp8_append_decode_supported, which depends on shapes only (cached per shape)."""
+    return _native.lib().kvfp8_append_decode_supported(b, hq, hkv, d, bt_rows, bt_width, block_size, kv_code) == 1
+
+
 def append_decode_attention(q, ks, vs, paged_kv_cache, cache_batch_context):
     """`paged_kv_cache.append_kv(ctx.physical_blocks, ctx.block_offsets, ks, vs)` followed by
     `decode_attention_wrapper(q, paged_kv_cache, ctx)`, the decode step of reference
@@ -184,9 +191,8 @@ def append_decode_attention(q, ks, vs, paged_kv_cache, cache_batch_context):
     if ks.shape != expected or vs.shape != expected:
         raise ValueError(f"append_decode_attention: new K/V must be {expected}")
     fused = (cache.quantized and ks.dtype in _Q_DTYPES and q.device.type == "cuda"
-             and _native.lib().kvfp8_append_decode_supported(
-                 b, hq, hkv, d, ctx.block_table.shape[0], ctx.block_table.shape[1], cache.block_size,
-                 _native.dtype_code(cache.k.dtype)) == 1)
+             and _fused_supported(b, hq, hkv, d, ctx.block_table.shape[0], ctx.block_table.shape[1],
+                                  cache.block_size, _native.dtype_code(cache.k.dtype)))
     if not fused:
         cache.append_kv(ctx.physical_blocks, ctx.block_offsets, ks, vs)
         return decode_attention_wrapper(q, cache, ctx)
