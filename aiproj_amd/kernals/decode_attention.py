@@ -91,6 +91,12 @@ class DecodeCall:
         _native.check(_native.lib().kvfp8_paged_decode_reduce(*self.args), "kvfp8_paged_decode_reduce")
 
 
+@functools.lru_cache(maxsize=256)
+def _workspace_bytes(b, hq, hkv, d, bt_width, block_size, kv_code) -> int:
+    """kvfp8_decode_workspace_bytes, which depends on shapes only (cached per shape)."""
+    return _native.lib().kvfp8_decode_workspace_bytes(b, hq, hkv, d, bt_width, block_size, kv_code)
+
+
 def prepare_decode(q, paged_kv_cache, cache_batch_context=None) -> DecodeCall:
     """Validate the arguments of `decode_attention_wrapper` (same forms, same
     asserts and errors), allocate its output and workspace, and return the
@@ -144,9 +150,8 @@ def prepare_decode(q, paged_kv_cache, cache_batch_context=None) -> DecodeCall:
     cache_slots = _index_tensor(cache_slots)
     context_lengths = _index_tensor(context_lengths)
 
-    lib = _native.lib()
     kv_code = _native.dtype_code(k_cache.dtype)
-    ws_bytes = lib.kvfp8_decode_workspace_bytes(b, hq, hkv, d, block_table.shape[1], block_size, kv_code)
+    ws_bytes = _workspace_bytes(b, hq, hkv, d, block_table.shape[1], block_size, kv_code)
     workspace = t.empty(max(ws_bytes, 1), dtype=t.uint8, device=q.device)
 
     args = (
