@@ -197,3 +197,33 @@ def test_row_division_special_rows_take_the_ieee_path(lib):
 
 def test_encoder_selftest_rejects_null(lib):
     assert lib.kvfp8_selftest_fp8_encoder(None, None) == -4
+
+
+def test_fused_append_and_swiglu_argument_checks(lib):
+    """Host-side answers of the fused append + decode entry points and the SwiGLU kernel:
+    shape support, and argument errors returned before any launch."""
+    fake = ctypes.c_void_p(16)    # never dereferenced: every call below fails host checks
+    supported = lib.kvfp8_append_decode_supported
+    assert supported(32, 32, 8, 128, 32, 257, 16, _native.E4M3FN) == 1
+    assert supported(4, 8, 2, 64, 4, 17, 16, _native.E4M3FN) == 1
+    assert supported(32, 32, 8, 128, 32, 257, 16, _native.BF16) == 0     # unquantized cache
+    assert supported(32, 32, 8, 96, 32, 257, 16, _native.E4M3FN) == 0     # head size
+    assert supported(32, 32, 8, 128, 32, 257, 12, _native.E4M3FN) == 0    # page size
+    assert supported(32, 30, 8, 128, 32, 257, 16, _native.E4M3FN) == 0    # group size
+
+    decode = [fake, _native.BF16, 0, 0, 4, 8, 2, 128, fake, fake, _native.E4M3FN, fake, fake,
+              64, 16, fake, 4, 64, fake, _native.I64, fake, _native.I32, 0.125, fake, fake, 1 << 30, None]
+    fused = lib.kvfp8_append_paged_decode
+    assert fused(*decode, fake, fake, _native.E4M3FN, 256, 128, 256, 128) == -1    # new-row dtype
+    assert fused(*decode, None, fake, _native.BF16, 256, 128, 256, 128) == -4      # no new rows
+    assert fused(*decode, fake, fake, _native.BF16, 256, 64, 256, 128) == -3       # heads not contiguous
+    bf16_cache = list(decode)
+    bf16_cache[10] = _native.BF16
+    assert fused(*bf16_cache, fake, fake, _native.BF16, 256, 128, 256, 128) == -2  # not on the fused kernel
+
+    silu = lib.kvfp8_silu_mul
+    assert silu(fake, _native.E4M3FN, 4, 8, 16, fake, 8, None) == -1
+    assert silu(fake, _native.BF16, -1, 8, 16, fake, 8, None) == -2
+    assert silu(fake, _native.BF16, 4, 8, 15, fake, 8, None) == -2                 # row shorter than 2 n
+    assert silu(None, _native.BF16, 4, 8, 16, fake, 8, None) == -4
+    assert silu(fake, _native.BF16, 0, 8, 16, fake, 8, None) == 0                  # nothing to do
