@@ -1,17 +1,16 @@
-"""Dense per-slot K/V cache, reference `src/torch_llm/inference/kv_cache.py:4-125`.
+"""Dense per-slot K/V cache: drop-in for reference `src/torch_llm/inference/kv_cache.py:4-125`.
 
-Layout (API, indexed directly by callers and tests):
+Storage (indexed directly by callers and tests):
     k_cache, v_cache  [batch_size, cache_max_seq_len, num_kv_heads, head_dim]  f16/bf16/f32
-    seq_lens          [batch_size] int32, tokens held per slot
+    seq_lens          [batch_size] int32, tokens held by each slot
 
-The reference keeps this dense cache beside the paged one as its simple
-reference; the continuous runtime uses `PagedKVCache`. The validation and its
-errors follow the reference line by line; like the reference, the capacity and
-slot checks read device values. The writes on a GPU are one launch of the HIP
-cast-and-scatter kernel (`kvfp8_store_append`), addressing the dense cache as
-`batch_size` pages of `cache_max_seq_len` slots: the row of a token is its
-cache slot and its column the slot's current length plus its offset in the
-prompt. Caches in host memory keep the reference's indexed store.
+The reference keeps this cache as the simple counterpart of `PagedKVCache`; its
+runtime uses the paged one. Both append forms reduce to one scatter: token i goes to
+row `slot_i`, column `seq_lens[slot_i] + (i - first token of its sequence)`. On a
+GPU the scatter is one launch of the cast-and-scatter kernel (`kvfp8_store_append`),
+which addresses the dense cache as `batch_size` pages of `cache_max_seq_len` rows;
+host-memory caches use an indexed store. The capacity and slot checks read device
+values, as the reference's do (this cache is not on the graph-captured path).
 """
 
 from __future__ import annotations
@@ -20,89 +19,94 @@ import torch as t
 
 from aiproj_amd.kernals.kv_cache.quantized_append import store_rows
 
+_STORAGE_DTYPES = (t.float16, t.bfloat16, t.float32)
+
 
 class KVCache:
-    """Dense reference cache. The continuous runtime uses PagedKVCache instead."""
+    """Dense cache with one row of `cache_max_seq_len` tokens per slot."""
 
     def __init__(self, batch_size, cache_max_seq_len, num_kv_heads, head_dim, dtype, device):
-        # Reference kv_cache.py:8-32.
-        for value in (batch_size, cache_max_seq_len, num_kv_heads, head_dim):
-            if not isinstance(value, int) or isinstance(value, bool) or value <= 0:
-                raise ValueError("Cache dimensions must be positive integers")
-        if dtype not in (t.float16, t.bfloat16, t.float32):
-            raise ValueError("Unsupported KV cache dtype")
-
-        self.batch_size = batch_size
-        self.cache_max_seq_len = cache_max_seq_len
-        self.num_kv_heads = num_kv_heads
-        self.head_dim = head_dim
-        self.k_cache = t.empty((batch_size, cache_max_seq_len, num_kv_heads, head_dim), dtype=dtype, device=device)
+        dims = (batch_size, cache_max_seq_len, num_kv_heads, head_dim)
+        if not all(isinstance(n, int) and not isinstance(n, bool) and n > 0 for n in dims):
+            raise ValueError(f"cache dimensions must be positive integers, got {dims}")
+        if dtype not in _STORAGE_DTYPES:
+            raise ValueError(f"KV cache dtype must be one of {_STORAGE_DTYPES}, got {dtype}")
+        self.batch_size, self.cache_max_seq_len, self.num_kv_heads, self.head_dim = dims
+        self.k_cache = t.empty(dims, dtype=dtype, device=device)
         self.v_cache = t.empty_like(self.k_cache)
         self.seq_lens = t.zeros(batch_size, dtype=t.int32, device=device)
 
+    @property
+    def _device(self):
+        return self.k_cache.device
+
     def slots(self, cache_slots):
-        """The slot indices a call addresses (all slots when None), reference kv_cache.py:35-56."""
+        """The slots a call addresses: all of them for None, else a vector of distinct
+        in-range int32/int64 indices (an empty vector is allowed)."""
         if cache_slots is None:
-            return t.arange(self.batch_size, device=self.k_cache.device)
-        slots = t.as_tensor(cache_slots, device=self.k_cache.device)
-        if slots.ndim != 1:
-            raise ValueError("cache_slots must be a vector of integer indices")
-        if slots.numel() == 0:
-            return slots.to(t.long)
-        if slots.dtype not in (t.int32, t.int64):
-            raise ValueError("cache_slots must be a vector of integer indices")
-        if not bool(((slots >= 0) & (slots < self.batch_size)).all()) or slots.unique().numel() != slots.numel():
-            raise ValueError("cache_slots must be unique, valid cache indices")
-        return slots
+            return t.arange(self.batch_size, device=self._device)
+        chosen = t.as_tensor(cache_slots, device=self._device)
+        if chosen.ndim != 1:
+            raise ValueError("cache_slots must be a 1-D vector of slot indices")
+        if chosen.numel() == 0:
+            return chosen.long()
+        if chosen.dtype not in (t.int32, t.int64):
+            raise ValueError(f"cache_slots must hold int32 or int64 indices, got {chosen.dtype}")
+        in_range = bool(((chosen >= 0) & (chosen < self.batch_size)).all())
+        if not in_range or chosen.unique().numel() != chosen.numel():
+            raise ValueError(f"cache_slots must be distinct indices in [0, {self.batch_size})")
+        return chosen
 
     def check_kv(self, new_k, new_v, num_tokens):
-        shape = (num_tokens, self.num_kv_heads, self.head_dim)
-        if new_k.shape != shape or new_v.shape != shape:
-            raise ValueError(f"Expected K/V shape {shape}")
-        if new_k.device != self.k_cache.device or new_v.device != self.k_cache.device:
-            raise ValueError("K/V must be on the cache device")
+        """New rows must be [num_tokens, num_kv_heads, head_dim] on the cache device."""
+        want = (num_tokens, self.num_kv_heads, self.head_dim)
+        if tuple(new_k.shape) != want or tuple(new_v.shape) != want:
+            raise ValueError(f"new K/V must have shape {want}, got {tuple(new_k.shape)} / {tuple(new_v.shape)}")
+        if new_k.device != self._device or new_v.device != self._device:
+            raise ValueError(f"new K/V must be on the cache device {self._device}")
 
-    def _store(self, rows, cols, new_k, new_v):
-        if self.k_cache.device.type == "cuda":
+    def _scatter(self, rows, cols, new_k, new_v):
+        if self._device.type == "cuda":
             store_rows(self.k_cache, self.v_cache, new_k, new_v, rows, cols, what="KVCache")
-        else:
-            self.k_cache[rows, cols] = new_k.to(self.k_cache.dtype)
-            self.v_cache[rows, cols] = new_v.to(self.v_cache.dtype)
+            return
+        dtype = self.k_cache.dtype
+        self.k_cache[rows, cols] = new_k.to(dtype)
+        self.v_cache[rows, cols] = new_v.to(dtype)
 
     @t.no_grad()
     def append_decode(self, new_k, new_v, cache_slots=None):
-        """One token per addressed slot at its current length, reference kv_cache.py:67-79."""
-        slots = self.slots(cache_slots)
-        self.check_kv(new_k, new_v, slots.numel())
-        positions = self.seq_lens[slots]
-        if not bool((positions < self.cache_max_seq_len).all()):
-            raise ValueError("Decode would exceed cache capacity")
-        self._store(slots, positions, new_k, new_v)
-        self.seq_lens[slots] += 1
+        """One new token for each addressed slot, stored at the slot's current length."""
+        rows = self.slots(cache_slots)
+        self.check_kv(new_k, new_v, rows.numel())
+        cols = self.seq_lens[rows]
+        if not bool((cols < self.cache_max_seq_len).all()):
+            raise ValueError(f"a decode token would pass the cache capacity {self.cache_max_seq_len}")
+        self._scatter(rows, cols, new_k, new_v)
+        self.seq_lens[rows] += 1
 
     @t.no_grad()
     def append_prefill(self, new_k, new_v, cu_seqlens, cache_slots=None):
-        """Packed prompts (cu_seqlens offsets) after each slot's current length,
-        reference kv_cache.py:82-118."""
-        slots = self.slots(cache_slots)
-        self.check_kv(new_k, new_v, new_k.shape[0])
-        if cu_seqlens.device != self.k_cache.device or cu_seqlens.dtype not in (t.int32, t.int64):
-            raise ValueError("cu_seqlens must be integer metadata on the cache device")
-        if cu_seqlens.shape != (slots.numel() + 1,):
-            raise ValueError("cu_seqlens must contain one boundary per request plus the end")
-        lengths = cu_seqlens[1:] - cu_seqlens[:-1]
-        if int(cu_seqlens[0]) != 0 or int(cu_seqlens[-1]) != new_k.shape[0] or not bool((lengths >= 0).all()):
-            raise ValueError("Invalid cumulative sequence lengths")
-        if not bool((self.seq_lens[slots] + lengths <= self.cache_max_seq_len).all()):
-            raise ValueError("Prefill would exceed cache capacity")
-
+        """Packed prompts: tokens cu_seqlens[i] .. cu_seqlens[i + 1] - 1 continue slot i's row."""
+        rows = self.slots(cache_slots)
         total = new_k.shape[0]
-        token_slots = t.repeat_interleave(slots, lengths, output_size=total)
-        starts = t.repeat_interleave(cu_seqlens[:-1], lengths, output_size=total)
-        positions = self.seq_lens[token_slots] + t.arange(total, device=self.k_cache.device) - starts
-        self._store(token_slots, positions, new_k, new_v)
-        self.seq_lens[slots] += lengths
+        self.check_kv(new_k, new_v, total)
+        if cu_seqlens.device != self._device or cu_seqlens.dtype not in (t.int32, t.int64):
+            raise ValueError(f"cu_seqlens must be an int32/int64 tensor on {self._device}")
+        if tuple(cu_seqlens.shape) != (rows.numel() + 1,):
+            raise ValueError(f"cu_seqlens must hold {rows.numel() + 1} boundaries (slots + 1)")
+        counts = cu_seqlens[1:] - cu_seqlens[:-1]
+        if int(cu_seqlens[0]) != 0 or int(cu_seqlens[-1]) != total or not bool((counts >= 0).all()):
+            raise ValueError("cu_seqlens must start at 0, end at the token count and never decrease")
+        if not bool((self.seq_lens[rows] + counts <= self.cache_max_seq_len).all()):
+            raise ValueError(f"a prompt would pass the cache capacity {self.cache_max_seq_len}")
+        # Column of token i: its slot's length plus its offset inside its own prompt.
+        owner = t.repeat_interleave(t.arange(rows.numel(), device=self._device), counts, output_size=total)
+        offset_in_prompt = t.arange(total, device=self._device) - cu_seqlens[owner]
+        token_rows = rows[owner]
+        self._scatter(token_rows, self.seq_lens[token_rows] + offset_in_prompt, new_k, new_v)
+        self.seq_lens[rows] += counts
 
     def clear(self, cache_slots=None):
-        # Stale storage is unreachable once the lengths are reset: no fill of the cache.
+        """Forget the addressed slots' tokens. Only the lengths reset: rows past a
+        slot's length are never read, so the storage is not zeroed."""
         self.seq_lens[self.slots(cache_slots)] = 0

@@ -176,11 +176,11 @@ def test_context_uses_full_slot_table_and_committed_history():
 def test_allocation_order_and_page_table_gather():
     manager = PageAllocator(10, 4, 2, 16, "cpu")
     s0 = manager.allocate_request(1, 9)          # 3 pages from the end of the free list
-    assert manager.slot_blocks[s0] == [7, 8, 9]
+    assert manager.get_block_table([s0])[0, :3].tolist() == [7, 8, 9]
     assert manager.block_table[s0, :3].tolist() == [7, 8, 9]
     assert manager.block_table[s0, 3:].tolist() == [-1]
     s1 = manager.allocate_request(2, 2)
-    assert manager.slot_blocks[s1] == [6]
+    assert manager.block_table[s1].tolist() == [6, -1, -1, -1]
     blocks, offsets = manager.get_physical_location(s0, t.arange(9))
     assert blocks.tolist() == [7] * 4 + [8] * 4 + [9]
     assert offsets.tolist() == [0, 1, 2, 3] * 2 + [0]
@@ -210,6 +210,167 @@ def test_resolve_batch_locations_expands_slots_per_token():
     assert offsets.tolist() == [0, 1, 1, 2, 2]
     with pytest.raises(ValueError):
         manager.resolve_batch_locations(t.tensor([a, b]), t.tensor([0, 3, 4], dtype=t.int32), positions)
+
+
+def test_cache_rejects_overflow_even_inside_last_partial_page():
+    """Reference tests/test_inference.py:322-334."""
+    manager = PageAllocator(2, 4, 1, 5, "cpu")
+    manager.allocate_request(1, 5)
+    manager.advance(1, 5)
+    with pytest.raises(CacheCapacityError):
+        manager.advance(1, 1)
+    assert manager.get_seq_len(1) == 5
+    with pytest.raises(ValueError):
+        manager.allocate_request(1, 2)
+    with pytest.raises(ValueError):
+        manager.reserve_capacity(0, -1)
+    manager.clear()
+    assert sorted(manager.free_blocks) == [0, 1]
+
+
+class _AllocatorModel:
+    """The allocator contract written as plain lists: a slot stack and a page stack
+    served from their ends, per-slot page lists and committed lengths."""
+
+    def __init__(self, num_blocks, block_size, slots, max_len):
+        self.bs, self.max_len = block_size, max_len
+        self.free_pages = list(range(num_blocks))
+        self.free_slots = list(range(slots))
+        self.owner, self.pages, self.length = {}, {}, {}
+
+    def need(self, n):
+        return -(-n // self.bs)
+
+    def allocate(self, rid, n):
+        if rid in self.owner or not 0 <= n <= self.max_len:
+            return "value"
+        if not self.free_slots or self.need(n) > len(self.free_pages):
+            return "capacity"
+        slot = self.free_slots.pop()
+        self.owner[rid] = slot
+        self.pages[slot] = [self.free_pages.pop() for _ in range(self.need(n))][::-1]
+        self.length[slot] = 0
+        return slot
+
+    def reserve(self, slots, lens):
+        if len(set(slots)) != len(slots) or any(s not in self.pages for s in slots):
+            return "value"
+        if any(not 0 <= n <= self.max_len for n in lens):
+            return "value"
+        extra = [max(0, self.need(n) - len(self.pages[s])) for s, n in zip(slots, lens)]
+        if sum(extra) > len(self.free_pages):
+            return "capacity"
+        for s, k in zip(slots, extra):
+            self.pages[s] += [self.free_pages.pop() for _ in range(k)][::-1]
+        return None
+
+    def advance(self, rid, n):
+        slot = self.owner[rid]
+        new = self.length[slot] + n
+        if new > min(self.max_len, len(self.pages[slot]) * self.bs):
+            return "capacity"
+        self.length[slot] = new
+        return None
+
+    def free(self, rid):
+        slot = self.owner.pop(rid)
+        self.free_pages += self.pages.pop(slot)
+        del self.length[slot]
+        self.free_slots.append(slot)
+
+
+def test_allocator_follows_the_contract_model_over_random_operations():
+    """Random allocate / reserve / advance / free sequences, including refused ones:
+    after every call the allocator's stacks, table rows and lengths equal the model's,
+    and a refused call changes nothing."""
+    import random
+
+    rng = random.Random(5)
+    manager = PageAllocator(24, 4, 5, 30, "cpu")
+    model = _AllocatorModel(24, 4, 5, 30)
+    errors = {"value": ValueError, "capacity": CacheCapacityError}
+    for step in range(3000):
+        op = rng.choice(["allocate", "allocate", "reserve", "advance", "advance", "free"])
+        live = list(model.owner)
+        if op == "allocate":
+            rid, n = rng.randrange(12), rng.randrange(-1, 33)
+            want = model.allocate(rid, n)
+            if want in errors:
+                with pytest.raises(errors[want]):
+                    manager.allocate_request(rid, n)
+            else:
+                assert manager.allocate_request(rid, n) == want
+        elif op == "reserve" and live:
+            chosen = rng.sample(live, rng.randint(1, len(live)))
+            slots = [model.owner[r] for r in chosen]
+            if rng.random() < 0.1:
+                slots.append(slots[0])                      # duplicate slot: refused
+            lens = [rng.randrange(0, 34) for _ in slots]
+            want = model.reserve(slots, lens)
+            if want is None:
+                manager.reserve_batch_capacity(slots, lens)
+            else:
+                with pytest.raises(errors[want]):
+                    manager.reserve_batch_capacity(slots, lens)
+        elif op == "advance" and live:
+            rid, n = rng.choice(live), rng.randrange(0, 12)
+            want = model.advance(rid, n)
+            if want is None:
+                manager.advance(rid, n)
+            else:
+                with pytest.raises(errors[want]):
+                    manager.advance(rid, n)
+        elif op == "free" and live:
+            rid = rng.choice(live)
+            model.free(rid)
+            manager.free_request(rid)
+        assert manager.free_blocks == model.free_pages, step
+        assert manager.free_slots == model.free_slots, step
+        assert manager.request_to_slot == model.owner, step
+        table = manager.block_table.tolist()
+        lengths = manager.seq_lens.tolist()
+        for slot in range(5):
+            pages = model.pages.get(slot, [])
+            assert table[slot] == pages + [-1] * (8 - len(pages)), step
+            assert lengths[slot] == model.length.get(slot, 0), step
+        for rid, slot in model.owner.items():
+            assert manager.get_seq_len(rid) == model.length[slot]
+
+
+def test_allocator_gather_matches_the_oracle():
+    import oracle
+
+    manager = PageAllocator(40, 4, 4, 32, "cpu")
+    for rid, n in enumerate([5, 32, 1, 17]):
+        manager.allocate_request(rid, n)
+    manager.free_request(2)
+    manager.allocate_request(9, 12)
+    table = manager.block_table.numpy()
+    for rid in (0, 1, 3, 9):
+        slot = manager.get_slot(rid)
+        reserved = 4 * int((table[slot] >= 0).sum())
+        positions = t.arange(reserved)
+        blocks, offsets = manager.get_physical_location(slot, positions)
+        o_blocks, o_offsets = oracle.physical_location(table, slot, positions.numpy(), 4)
+        assert blocks.tolist() == o_blocks.tolist() and offsets.tolist() == o_offsets.tolist()
+
+
+def test_container_marks_decode_steps_that_append_at_the_last_position():
+    manager = PageAllocator(16, 4, 3, 32, "cpu")
+    a = manager.allocate_request(0, 12)
+    b = manager.allocate_request(1, 12)
+    manager.advance(0, 5)
+    manager.advance(1, 9)
+    slots = t.tensor([a, b])
+    one_each = t.tensor([0, 1, 2], dtype=t.int32)
+    ctx = manager.create_container(slots, one_each, t.tensor([5, 9]))
+    assert ctx.appends_last_position
+    assert ctx.context_lengths.tolist() == [6, 10]
+    # A write anywhere else, several tokens per sequence, or unvalidated metadata: no mark.
+    assert not manager.create_container(slots, one_each, t.tensor([5, 3])).appends_last_position
+    assert not manager.create_container(slots, t.tensor([0, 2, 3], dtype=t.int32),
+                                        t.tensor([5, 6, 9])).appends_last_position
+    assert not manager.create_container(slots, one_each, t.tensor([5, 9]), validate=False).appends_last_position
 
 
 def test_rmsnorm_validates_on_the_host_and_refuses_cpu_tensors():
