@@ -208,6 +208,9 @@ struct NewTokens {
     const void* v;
     int dtype;
     int32_t k_sb, v_sb;
+    const void* blocks;
+    const void* offsets;
+    int blocks64, offsets64;
 };
 
 struct Plan {
@@ -241,7 +244,7 @@ int64_t generic_workspace(const Plan& p, int32_t batch, int32_t hq, int32_t d) {
 }
 
 // The MFMA path falls back to the generic kernel when a pointer is not 16-byte
-// aligned, so its workspace covers both.
+// aligned, so the size quoted from shapes alone covers both.
 int64_t workspace_for(const Plan& p, int32_t batch, int32_t hq, int32_t hkv, int32_t d) {
     int64_t need = generic_workspace(p, batch, hq, d);
     if (p.mfma) {
@@ -375,14 +378,19 @@ extern "C" int kvfp8_append_decode_supported(int32_t batch, int32_t num_q_heads,
 
 extern "C" int kvfp8_append_paged_decode(KVFP8_DECODE_PARAMS, const void* k_new, const void* v_new, int new_dtype,
                                          int64_t k_new_stride_b, int64_t k_new_stride_h, int64_t v_new_stride_b,
-                                         int64_t v_new_stride_h) {
+                                         int64_t v_new_stride_h, const void* new_blocks, int new_blocks_dtype,
+                                         const void* new_offsets, int new_offsets_dtype) {
     if (new_dtype != KVFP8_F32 && new_dtype != KVFP8_F16 && new_dtype != KVFP8_BF16) return KVFP8_EDTYPE;
-    if (batch > 0 && (!k_new || !v_new)) return KVFP8_ENULL;
+    if ((new_blocks_dtype != KVFP8_I32 && new_blocks_dtype != KVFP8_I64) ||
+        (new_offsets_dtype != KVFP8_I32 && new_offsets_dtype != KVFP8_I64))
+        return KVFP8_EDTYPE;
+    if (batch > 0 && (!k_new || !v_new || !new_blocks || !new_offsets)) return KVFP8_ENULL;
     // Heads are contiguous within a row; row strides are int32 element counts.
     if (k_new_stride_h != head_dim || v_new_stride_h != head_dim || k_new_stride_b < 0 || v_new_stride_b < 0 ||
         k_new_stride_b > INT32_MAX || v_new_stride_b > INT32_MAX)
         return KVFP8_ESTRIDE;
-    const NewTokens fresh{k_new, v_new, new_dtype, (int32_t)k_new_stride_b, (int32_t)v_new_stride_b};
+    const NewTokens fresh{k_new, v_new, new_dtype, (int32_t)k_new_stride_b, (int32_t)v_new_stride_b,
+                          new_blocks, new_offsets, new_blocks_dtype == KVFP8_I64, new_offsets_dtype == KVFP8_I64};
     return paged_decode(KVFP8_DECODE_ARGS, kPhaseSplit | kPhaseReduce, &fresh);
 }
 
@@ -450,6 +458,10 @@ int paged_decode(const void* q, int q_dtype, int64_t q_stride_b, int64_t q_strid
     a.new_dtype = fresh ? fresh->dtype : KVFP8_BF16;
     a.new_k_sb = fresh ? fresh->k_sb : 0;
     a.new_v_sb = fresh ? fresh->v_sb : 0;
+    a.new_blocks = fresh ? fresh->blocks : nullptr;
+    a.new_offsets = fresh ? fresh->offsets : nullptr;
+    a.new_blocks64 = fresh ? fresh->blocks64 : 0;
+    a.new_offsets64 = fresh ? fresh->offsets64 : 0;
 
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     hipError_t err;

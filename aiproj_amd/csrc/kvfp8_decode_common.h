@@ -45,12 +45,16 @@ struct DecodeArgs {
     int32_t max_chunks;       // ceil(bt_width * block_size / chunk_tokens)
     // Fused append (kvfp8_append_paged_decode): the new token of every sequence,
     // rows [batch, Hkv, D] with element strides (row stride, D, 1), quantized into
-    // the cache at position context_lengths[b] - 1 before it is attended. Read only
-    // by the kernels built for the fused call.
+    // the cache at (new_blocks[b], new_offsets[b]), the sequence's last attended
+    // position, before it is attended. Read only by the kernels built for the fused
+    // call.
     const void* new_k;
     const void* new_v;
     int32_t new_dtype;
     int32_t new_k_sb, new_v_sb;
+    const void* new_blocks;
+    const void* new_offsets;
+    int32_t new_blocks64, new_offsets64;
 };
 
 __device__ __forceinline__ int64_t load_i(const void* p, int is64, int64_t i) {

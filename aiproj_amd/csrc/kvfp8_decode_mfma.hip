@@ -571,6 +571,10 @@ __device__ __forceinline__ void compute_step(WaveState<C>& st, const StepData<C,
 // arithmetic as quantize_append_kernel (amax as an integer max of |x| bits, which
 // propagates NaN; scale = amax / 448 by IEEE division, 1 when amax is 0 or NaN;
 // codes from the corrected reciprocal on finite rows, else clamp and encode).
+// The row goes where the caller's write location (new_blocks[b], new_offsets[b])
+// points, and nowhere when that lies outside the pool, as in the append kernel.
+// The caller guarantees that this location is the sequence's last attended
+// position, so it lies in the tile this wave reads last.
 // Lane l holds elements C l .. C l + C - 1. fetch() issues the loads and put()
 // quantizes and stores; the wave's own loads of that page row come after put()
 // in its instruction order, which the memory pipeline keeps for one wave, so
@@ -584,20 +588,9 @@ struct NewRow {
 typedef const __attribute__((address_space(4))) int64_t* const_i64_ptr;
 
 template <int C>
-__device__ __forceinline__ void fetch_new_token(const MfmaArgs& a, int b, int h, const int32_t* table_row,
-                                                int64_t len, int lane, NewRow<C>& r) {
+__device__ __forceinline__ void fetch_new_token(const MfmaArgs& a, int b, int h, int lane, NewRow<C>& r) {
     constexpr int D = 64 * C;
     r.row = -1;
-    // Only where the length was not clipped to the table (scalar loads: their wait
-    // does not cover the vector loads in flight).
-    const int64_t caddr = uniform64((int64_t)(uintptr_t)a.d.ctx);
-    const int64_t ctx = a.d.ctx64 ? ((const_i64_ptr)(uintptr_t)caddr)[b] : (int64_t)((const_i32_ptr)(uintptr_t)caddr)[b];
-    if (ctx != len) return;
-    const int64_t pos = len - 1;
-    const int64_t addr = uniform64((int64_t)(uintptr_t)(table_row + (pos >> a.d.bs_shift)));
-    const int64_t page = *(const_i32_ptr)(uintptr_t)addr;
-    if (page < 0 || page >= a.d.num_blocks) return;           // the reads skip this page too
-    r.row = ((page << a.d.bs_shift) + (pos & (a.d.block_size - 1))) * a.d.num_kv_heads + h;
     // The new-row fields are read from the kernel-argument segment here, where they
     // are used: the empty asm keeps the compiler from hoisting these loads to the
     // kernel's entry and holding them in scalar registers through the step loop.
@@ -605,17 +598,24 @@ __device__ __forceinline__ void fetch_new_token(const MfmaArgs& a, int b, int h,
     __asm__ volatile("" : "+s"(kargs));
     typedef const __attribute__((address_space(4))) DecodeArgs* const_args_ptr;
     const_args_ptr na = (const_args_ptr)(uintptr_t)(kargs + offsetof(MfmaArgs, d));
+    // Write location: scalar loads (their wait does not cover the vector loads in
+    // flight). The index arrays are read-only for the whole kernel.
+    const uint64_t pb = (uint64_t)(uintptr_t)na->new_blocks, po = (uint64_t)(uintptr_t)na->new_offsets;
+    const int64_t page = na->new_blocks64 ? ((const_i64_ptr)pb)[b] : (int64_t)((const_i32_ptr)pb)[b];
+    const int64_t off = na->new_offsets64 ? ((const_i64_ptr)po)[b] : (int64_t)((const_i32_ptr)po)[b];
+    if (page < 0 || page >= a.d.num_blocks || off < 0 || off >= a.d.block_size) return;
+    r.row = (page * a.d.block_size + off) * a.d.num_kv_heads + h;
     const int dtype = na->new_dtype;
 #pragma unroll
     for (int kv = 0; kv < 2; ++kv) {
-        const int64_t off = (int64_t)b * (kv ? na->new_v_sb : na->new_k_sb) + (int64_t)h * D + C * lane;
+        const int64_t src_off = (int64_t)b * (kv ? na->new_v_sb : na->new_k_sb) + (int64_t)h * D + C * lane;
         const void* src = kv ? na->new_v : na->new_k;
         float* x = kv ? r.v : r.k;
 #pragma unroll
         for (int e = 0; e < C; ++e)
-            x[e] = dtype == KVFP8_F32 ? reinterpret_cast<const float*>(src)[off + e]
-                 : dtype == KVFP8_F16 ? f16_to_f32(reinterpret_cast<const uint16_t*>(src)[off + e])
-                                      : bf16_to_f32(reinterpret_cast<const uint16_t*>(src)[off + e]);
+            x[e] = dtype == KVFP8_F32 ? reinterpret_cast<const float*>(src)[src_off + e]
+                 : dtype == KVFP8_F16 ? f16_to_f32(reinterpret_cast<const uint16_t*>(src)[src_off + e])
+                                      : bf16_to_f32(reinterpret_cast<const uint16_t*>(src)[src_off + e]);
     }
 }
 
@@ -680,6 +680,19 @@ decode_mfma_kernel(MfmaArgs a) {
     const int G = a.d.num_q_heads / a.d.num_kv_heads;
     float4* stage = stage_all[wave];
 
+    if constexpr (kAppend) {
+        // Sequences with no attended tile are read by no workgroup; their new rows
+        // are still written (workgroup b % groups writes sequence b).
+        for (int b = w; b < a.d.batch; b += groups) {
+            if (uniform(prefix[b + 1]) != uniform(prefix[b])) continue;
+            for (int h = wave; h < a.d.num_kv_heads; h += waves) {
+                NewRow<C> fresh;
+                fetch_new_token<C>(a, uniform(b), h, lane, fresh);
+                put_new_token<C>(a, fresh, lane);
+            }
+        }
+    }
+
     // Waves w and w + 4 share a SIMD, whose arbiter favours the older wave: left
     // alone, waves 0-3 finish their (equal) work about 10% before waves 4-7 and the
     // CU streams with half its waves for the rest of the range. After every step a
@@ -723,7 +736,7 @@ decode_mfma_kernel(MfmaArgs a) {
             const bool append = kAppend && seg1 == seq1;
             NewRow<C> fresh;
             if constexpr (kAppend) {
-                if (append) fetch_new_token<C>(a, b, h, table_row, len, lane, fresh);
+                if (append) fetch_new_token<C>(a, b, h, lane, fresh);
             }
             const bool put_early = t1 - 1 < t0 + (ES == 1 ? 4 : 2);
             if constexpr (kAppend) {

@@ -15,8 +15,10 @@ what drives the FP8 paged KV-cache path:
   that live as long as the decoder, so the step can be captured once in a HIP
   graph and replayed (`capture()`, `generate()`).
 
-Unlike the reference runtime, the allocator's host-side lengths are advanced once
-after generation instead of every step (they are not read during it).
+Unlike the reference runtime, the allocator's committed lengths are not advanced
+by every step (that would be host work inside the captured step): `generate()`
+commits the tokens it wrote when it returns, and a caller driving `step()` itself
+commits with `commit(steps)`.
 """
 
 from __future__ import annotations
@@ -78,7 +80,8 @@ class GreedyDecoder:
         table = self.allocator.block_table
         blocks = table[self.slots, self.positions // self.block_size]
         offsets = self.positions % self.block_size
-        ctx = CacheContainer(self.slots, blocks, offsets, self.context_lengths, table)
+        # The new token of every sequence is written at its last attended position.
+        ctx = CacheContainer(self.slots, blocks, offsets, self.context_lengths, table, appends_last_position=True)
         meta = StepMeta("decode", self.positions, ctx)
         logits = self.model(self.tokens, meta, self.caches)
         nxt = logits.argmax(-1)
@@ -111,4 +114,10 @@ class GreedyDecoder:
             else:
                 self.graph.replay()
         self.steps_left -= steps
+        self.commit(steps)
         return self.history[start:start + steps]
+
+    def commit(self, steps: int):
+        """Advance the allocator's committed lengths (host and device) by the `steps`
+        tokens each sequence's decode steps wrote into the cache."""
+        self.allocator.advance_batch(list(range(self.batch)), [steps] * self.batch)

@@ -182,12 +182,16 @@ def append_decode_attention(q, ks, vs, paged_kv_cache, cache_batch_context):
     `decode_attention_wrapper(q, paged_kv_cache, ctx)`, the decode step of reference
     `model/attention.py:86-99`, with the same results (cache codes and scales bit-identical).
 
-    ks, vs: [B, Hkv, D], the new token of every sequence of the batch. The fused form
-    writes the new token of sequence b at its last attended position, context_lengths[b] - 1
-    through the block table, which is where a decode step's write locations point
-    (`PageAllocator.resolve_batch_locations`: the position of the new token is the
-    committed length, and the context length is that plus one); it is taken on e4m3fn
-    caches whose shapes the MFMA kernel handles, and the two calls are made otherwise.
+    ks, vs: [B, Hkv, D], the new token of every sequence of the batch.
+
+    The write happens inside the decode kernel (one call, no separate append launch)
+    when the container says its write locations are the sequences' last attended
+    positions (`appends_last_position`: set by `PageAllocator.create_container` after
+    validating a one-token-per-sequence batch at the committed lengths, and by the
+    runtime's decode step, which builds such metadata) and the cache is e4m3fn with a
+    shape the MFMA kernel handles. The kernel writes row b at
+    (physical_blocks[b], block_offsets[b]), so the cache holds what the two calls would
+    write. Every other case makes the two calls.
     """
     cache, ctx = paged_kv_cache, cache_batch_context
     b, hq, d = q.shape
@@ -195,24 +199,31 @@ def append_decode_attention(q, ks, vs, paged_kv_cache, cache_batch_context):
     expected = (b, hkv, d)
     if ks.shape != expected or vs.shape != expected:
         raise ValueError(f"append_decode_attention: new K/V must be {expected}")
-    fused = (cache.quantized and ks.dtype in _Q_DTYPES and q.device.type == "cuda"
+    blocks, offsets = ctx.physical_blocks, ctx.block_offsets
+    fused = (getattr(ctx, "appends_last_position", False)
+             and cache.quantized and ks.dtype in _Q_DTYPES and vs.dtype in _Q_DTYPES
+             and q.device.type == "cuda" and blocks.shape == (b,) and offsets.shape == (b,)
              and _fused_supported(b, hq, hkv, d, ctx.block_table.shape[0], ctx.block_table.shape[1],
                                   cache.block_size, _native.dtype_code(cache.k.dtype)))
     if not fused:
-        cache.append_kv(ctx.physical_blocks, ctx.block_offsets, ks, vs)
+        cache.append_kv(blocks, offsets, ks, vs)
         return decode_attention_wrapper(q, cache, ctx)
-    _native.require_gpu(ks, vs, cache.k, what="append_decode_attention")
+    _native.require_gpu(ks, vs, cache.k, blocks, offsets, what="append_decode_attention")
     call = prepare_decode(q, cache, ctx)
     if call.args is None:
         return call.output
     if vs.dtype != ks.dtype:
-        vs = vs.to(ks.dtype)
+        # One dtype for both rows: float32 holds f16 and bf16 values exactly, so
+        # neither row is rounded again before it is quantized.
+        ks, vs = ks.float(), vs.float()
     if ks.stride(2) != 1 or ks.stride(1) != d:
         ks = ks.contiguous()
     if vs.stride(2) != 1 or vs.stride(1) != d:
         vs = vs.contiguous()
+    blocks, offsets = _index_tensor(blocks), _index_tensor(offsets)
     rc = _native.lib().kvfp8_append_paged_decode(
         *call.args, ks.data_ptr(), vs.data_ptr(), _native.dtype_code(ks.dtype),
-        ks.stride(0), ks.stride(1), vs.stride(0), vs.stride(1))
+        ks.stride(0), ks.stride(1), vs.stride(0), vs.stride(1),
+        blocks.data_ptr(), _native.dtype_code(blocks.dtype), offsets.data_ptr(), _native.dtype_code(offsets.dtype))
     _native.check(rc, "kvfp8_append_paged_decode")
     return call.output

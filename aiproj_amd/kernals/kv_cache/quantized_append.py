@@ -35,6 +35,15 @@ def _prepare_input(x: t.Tensor) -> t.Tensor:
     return x
 
 
+def _same_dtype(ks: t.Tensor, vs: t.Tensor):
+    """K and V in one dtype for the kernel, with neither rounded again: when they
+    differ both become float32, which holds every f16 and bf16 value exactly (the
+    reference converts each input to float32 on its own)."""
+    if ks.dtype == vs.dtype:
+        return ks, vs
+    return ks.float(), vs.float()
+
+
 def quantize_append_wrapper(
     paged_kv_cache,
     ks,
@@ -53,9 +62,7 @@ def quantize_append_wrapper(
                                  what="quantize_append_wrapper")
     if num_tokens == 0:
         return
-    ks, vs = _prepare_input(ks), _prepare_input(vs)
-    if vs.dtype != ks.dtype:
-        vs = vs.to(ks.dtype)
+    ks, vs = _same_dtype(_prepare_input(ks), _prepare_input(vs))
 
     lib = _native.lib()
     rc = lib.kvfp8_quantize_append(
@@ -91,9 +98,7 @@ def store_rows(k_cache, v_cache, ks, vs, rows, cols, what="store_rows"):
     device = _native.require_gpu(ks, vs, rows, cols, k_cache, what=what)
     if num_tokens == 0:
         return
-    ks, vs = _prepare_input(ks), _prepare_input(vs)
-    if vs.dtype != ks.dtype:
-        vs = vs.to(ks.dtype)
+    ks, vs = _same_dtype(_prepare_input(ks), _prepare_input(vs))
     lib = _native.lib()
     rc = lib.kvfp8_store_append(
         ks.data_ptr(), vs.data_ptr(), _native.dtype_code(ks.dtype),

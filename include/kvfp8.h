@@ -215,17 +215,20 @@ int kvfp8_prefill_attention(const void* q_dev, const void* k_dev, const void* v_
  *
  * Replaces the two calls the reference makes back to back in its decode step,
  * reference src/torch_llm/model/attention.py:86-99 (PagedKVCache.append_kv, then
- * decode_attention_wrapper), for the case where the new token of sequence b is
- * its last attended position: it is written at position context_lengths[b] - 1,
- * page block_table[slots[b], (context_lengths[b] - 1) / block_size], with the
- * kvfp8_quantize_append rule (codes and scales bit-identical to it), before the
- * attention reads it. A sequence whose length is 0, is clipped to the table
- * width, or whose last page is outside [0, num_blocks) gets no write.
+ * decode_attention_wrapper). Row b of k_new/v_new is written at
+ * (new_blocks[b], new_offsets[b]) with the kvfp8_quantize_append rule (codes and
+ * scales bit-identical to it; locations outside the pool are skipped), before the
+ * attention reads it. The caller guarantees that this location is sequence b's last
+ * attended position, page block_table[slots[b], (context_lengths[b] - 1) /
+ * block_size] at offset (context_lengths[b] - 1) % block_size: the write is ordered
+ * before the reads of that position only. With that guarantee the results equal the
+ * two calls bit for bit.
  *
  * Takes the kvfp8_paged_decode arguments, then the new rows: k_new/v_new
- * [batch, H_kv, D] (f32/f16/bf16) with element strides (stride_b, stride_h, 1),
- * stride_h == D and stride_b below 2^31. e4m3fn caches on the MFMA kernel only:
- * other shapes return KVFP8_ESHAPE before launching anything
+ * [batch, H_kv, D] (f32/f16/bf16, one dtype) with element strides (stride_b,
+ * stride_h, 1), stride_h == D and stride_b below 2^31, then the write locations
+ * new_blocks/new_offsets [batch] (int32/int64). e4m3fn caches on the MFMA kernel
+ * only: other shapes return KVFP8_ESHAPE before launching anything
  * (kvfp8_append_decode_supported says which).
  */
 int kvfp8_append_paged_decode(const void* q_dev, int q_dtype, int64_t q_stride_b, int64_t q_stride_h,
@@ -240,7 +243,9 @@ int kvfp8_append_paged_decode(const void* q_dev, int q_dtype, int64_t q_stride_b
                               void* workspace_dev, int64_t workspace_bytes, void* stream,
                               const void* k_new_dev, const void* v_new_dev, int new_dtype,
                               int64_t k_new_stride_b, int64_t k_new_stride_h,
-                              int64_t v_new_stride_b, int64_t v_new_stride_h);
+                              int64_t v_new_stride_b, int64_t v_new_stride_h,
+                              const void* new_blocks_dev, int new_blocks_dtype,
+                              const void* new_offsets_dev, int new_offsets_dtype);
 
 /* 1 when kvfp8_append_paged_decode handles these shapes (e4m3fn cache on the MFMA
  * kernel), else 0. Shapes only; pointer alignment is checked by the call. */

@@ -214,12 +214,17 @@ def test_fused_append_and_swiglu_argument_checks(lib):
     decode = [fake, _native.BF16, 0, 0, 4, 8, 2, 128, fake, fake, _native.E4M3FN, fake, fake,
               64, 16, fake, 4, 64, fake, _native.I64, fake, _native.I32, 0.125, fake, fake, 1 << 30, None]
     fused = lib.kvfp8_append_paged_decode
-    assert fused(*decode, fake, fake, _native.E4M3FN, 256, 128, 256, 128) == -1    # new-row dtype
-    assert fused(*decode, None, fake, _native.BF16, 256, 128, 256, 128) == -4      # no new rows
-    assert fused(*decode, fake, fake, _native.BF16, 256, 64, 256, 128) == -3       # heads not contiguous
+    where = (fake, _native.I64, fake, _native.I32)                                 # write locations
+    assert fused(*decode, fake, fake, _native.E4M3FN, 256, 128, 256, 128, *where) == -1    # new-row dtype
+    assert fused(*decode, fake, fake, _native.BF16, 256, 128, 256, 128,
+                 fake, _native.F32, fake, _native.I32) == -1                               # location dtype
+    assert fused(*decode, None, fake, _native.BF16, 256, 128, 256, 128, *where) == -4      # no new rows
+    assert fused(*decode, fake, fake, _native.BF16, 256, 128, 256, 128,
+                 None, _native.I64, fake, _native.I32) == -4                               # no locations
+    assert fused(*decode, fake, fake, _native.BF16, 256, 64, 256, 128, *where) == -3       # heads not contiguous
     bf16_cache = list(decode)
     bf16_cache[10] = _native.BF16
-    assert fused(*bf16_cache, fake, fake, _native.BF16, 256, 128, 256, 128) == -2  # not on the fused kernel
+    assert fused(*bf16_cache, fake, fake, _native.BF16, 256, 128, 256, 128, *where) == -2  # not on the fused kernel
 
     silu = lib.kvfp8_silu_mul
     assert silu(fake, _native.E4M3FN, 4, 8, 16, fake, 8, None) == -1
