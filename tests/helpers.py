@@ -87,3 +87,33 @@ def torch_prefill_attention(q: t.Tensor, k: t.Tensor, v: t.Tensor, seq_lens: lis
         start = end
         i += n
     return out
+
+
+def torch_paged_decode(q: t.Tensor, cache, slots: t.Tensor, lengths: t.Tensor, block_table: t.Tensor) -> t.Tensor:
+    """Dequantize-then-attend in float32 on the device (the reference's CPU test oracle,
+    `tests/test_kv_cache_quantization.py:428-446`, batched): every sequence's K/V rows
+    gathered through its block-table row, `codes * scale` for an FP8 cache, GQA
+    softmax(q k^T / sqrt(D)) v over its first `lengths[b]` positions. -> [B, Hq, D] float32."""
+    b, hq, d = q.shape
+    hkv = cache.k.shape[2]
+    bs = cache.block_size
+    lengths = lengths.long()
+    width = int(lengths.max())
+    pos = t.arange(width, device=q.device)
+    rows = block_table[slots.long()][:, pos // bs].long().clamp_min(0)            # [B, W]
+    offs = (pos % bs).expand(b, width)
+
+    def gather(values, scales):
+        x = values[rows, offs].float()                                            # [B, W, Hkv, D]
+        if scales is not None:
+            x = x * scales[rows, offs].unsqueeze(-1)
+        return x
+
+    k = gather(cache.k, cache.k_scales).permute(0, 2, 3, 1).contiguous()          # [B, Hkv, D, W]
+    v = gather(cache.v, cache.v_scales).permute(0, 2, 1, 3).contiguous()          # [B, Hkv, W, D]
+    qg = q.float().view(b, hkv, hq // hkv, d)
+    scores = t.matmul(qg, k) / math.sqrt(d)                                       # [B, Hkv, G, W]
+    live = (pos[None, :] < lengths[:, None])[:, None, None, :]
+    scores = scores.masked_fill(~live, float("-inf"))
+    probs = t.nan_to_num(scores.softmax(dim=-1), nan=0.0)
+    return t.matmul(probs, v).reshape(b, hq, d)

@@ -301,6 +301,86 @@ def test_algorithmic_bytes_north_star():
     assert abs(nbytes / 1e6 - 277.4) < 0.1
 
 
+@pytest.mark.parametrize("kv_dtype", [np.uint8, np.float16])
+def test_decode_bytes_equal_the_arrays_one_call_touches(kv_dtype):
+    """The byte count of a decode call, recounted from numpy `nbytes` of what the
+    oracle gathers: every attended K and V row and its scale (fp8 only), q, the
+    output, and the block-table entry of every attended page."""
+    rng = np.random.default_rng(12)
+    lengths = [0, 1, 15, 16, 17, 100]
+    hq, hkv, d, bs = 8, 2, 24, 16
+    q, kc, vc, ks, vs, table = _random_paged(rng, lengths, hq, hkv, d, bs)
+    quantized = kv_dtype == np.uint8
+    if not quantized:
+        kc, vc, ks, vs = kc.astype(kv_dtype), vc.astype(kv_dtype), None, None
+    q16 = q.astype(np.float16)
+    touched = q16.nbytes + np.zeros((len(lengths), hq, d), np.float16).nbytes
+    for b, n in enumerate(lengths):
+        pos = np.arange(n)
+        pages = table[b, pos // bs]
+        touched += np.unique(pages).size * table.itemsize
+        for cache in (kc, vc):
+            touched += cache[pages, pos % bs].nbytes
+        if quantized:
+            touched += ks[pages, pos % bs].nbytes + vs[pages, pos % bs].nbytes
+    got = oracle.decode_algorithmic_bytes(lengths, hq, hkv, d, bs, q_bytes=2, out_bytes=2,
+                                          kv_bytes=np.dtype(kv_dtype).itemsize)
+    assert got == touched
+
+
+@pytest.mark.parametrize("in_dtype", [np.float32, np.float16])
+def test_append_bytes_equal_the_arrays_one_call_touches(in_dtype):
+    """The byte count of a quantize-and-scatter call, recounted from numpy `nbytes`:
+    the K and V rows read in their input dtype, and the cache codes and scales the
+    oracle's scatter writes (read back from the cache slices it changed)."""
+    rng = np.random.default_rng(13)
+    nb, bs, hkv, d, tokens = 9, 4, 3, 40, 17
+    k_cache = np.zeros((nb, bs, hkv, d), np.uint8)
+    v_cache = k_cache.copy()
+    k_scales = np.zeros((nb, bs, hkv), np.float32)
+    v_scales = k_scales.copy()
+    flat = rng.permutation(nb * bs)[:tokens]
+    blocks, offsets = flat // bs, flat % bs
+    ks = rng.standard_normal((tokens, hkv, d)).astype(in_dtype)
+    vs = rng.standard_normal((tokens, hkv, d)).astype(in_dtype)
+    oracle.scatter_append(k_cache, v_cache, k_scales, v_scales, ks.astype(np.float32), vs.astype(np.float32),
+                          blocks, offsets)
+    written = sum(x[blocks, offsets].nbytes for x in (k_cache, v_cache, k_scales, v_scales))
+    got = oracle.append_algorithmic_bytes(tokens, hkv, d, in_bytes=np.dtype(in_dtype).itemsize)
+    assert got == ks.nbytes + vs.nbytes + written
+    # And the cfg5 prefill write: 65,536 tokens x 4 heads x (2 x 128 x 2 + 2 x 128 + 8) = 203.4 MB.
+    assert oracle.append_algorithmic_bytes(65536, 4, 128) == 65536 * 4 * 776
+
+
+# ---------------------------------------------------------------------------
+# Page-table gather (reference inference/page_allocator.py:225-245)
+# ---------------------------------------------------------------------------
+
+def test_physical_location_matches_a_page_walk():
+    """Walking a slot's positions one at a time, with an offset counter that wraps
+    at the page size and a page counter that advances on the wrap, visits the
+    pages of the table row in order: the oracle's (page, offset) must agree at
+    every position, for scalar and broadcast (slot, position) arguments."""
+    rng = np.random.default_rng(14)
+    for bs, width, slots in ((1, 7, 2), (4, 5, 3), (16, 3, 4)):
+        table = rng.permutation(slots * width + 3)[:slots * width].reshape(slots, width).astype(np.int32)
+        positions = np.arange(width * bs)
+        for slot in range(slots):
+            blocks, offsets = oracle.physical_location(table, slot, positions, bs)
+            page_index, offset = 0, 0
+            for pos in positions:
+                assert (blocks[pos], offsets[pos]) == (table[slot, page_index], offset)
+                offset += 1
+                if offset == bs:
+                    offset, page_index = 0, page_index + 1
+        # A (slot, position) grid: every pair lands on its own cache row.
+        grid_slots = np.repeat(np.arange(slots), width * bs)
+        grid_pos = np.tile(positions, slots)
+        blocks, offsets = oracle.physical_location(table, grid_slots, grid_pos, bs)
+        rows = blocks * bs + offsets
+        assert np.unique(rows).size == rows.size
+
+
 # ---------------------------------------------------------------------------
 # Causal varlen (prefill) attention
 # ---------------------------------------------------------------------------
