@@ -22,6 +22,7 @@
 #include "kvfp8_decode_common.h"
 #include "kvfp8_decode_mfma.h"
 
+#include <mutex>
 #include <vector>
 
 namespace kvfp8 {
@@ -255,6 +256,44 @@ int64_t workspace_for(const Plan& p, int32_t batch, int32_t hq, int32_t hkv, int
     return need;
 }
 
+// What the kernel a call actually takes needs (its pointers decide MFMA or generic).
+int64_t workspace_taken(const Plan& p, bool mfma, int32_t batch, int32_t hq, int32_t hkv, int32_t d) {
+    if (!mfma) return generic_workspace(p, batch, hq, d);
+    int64_t off[4];
+    return mfma_workspace_layout(batch, hq, hkv, d, off);
+}
+
+// Workspace of kvfp8_paged_decode_noalloc: one static array per device, in place
+// of a caller's allocation. Host code never uses the symbol itself (its host-side
+// name is a stand-in, not a device address): the address comes from
+// hipGetSymbolAddress, fetched once per device with that device current and kept
+// in scratch_ptr. Nothing in it needs clearing: the decode kernels write every
+// byte they read back (tile plan, then partial states) within one call.
+constexpr int64_t kScratchBytes = KVFP8_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+void* scratch_ptr[kMaxDevices] = {};
+std::mutex scratch_mutex;
+
+// The current device's scratch address, looked up on the first call per device.
+int device_scratch(void** out) {
+    int dev = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return (int)err;
+    if (dev < 0 || dev >= kMaxDevices) return KVFP8_ELIMIT;
+    std::lock_guard<std::mutex> lock(scratch_mutex);
+    if (scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (err != hipSuccess) return (int)err;
+        if (p == nullptr) return (int)hipErrorInvalidSymbol;
+        scratch_ptr[dev] = p;
+    }
+    *out = scratch_ptr[dev];
+    return KVFP8_OK;
+}
+
 template <int KVT, int QT>
 hipError_t launch_generic(const DecodeArgs& a, int64_t units_total, hipStream_t s) {
     const size_t lds = (size_t)(a.batch + 1) * sizeof(int32_t);
@@ -326,7 +365,7 @@ int paged_decode(const void* q, int q_dtype, int64_t q_stride_b, int64_t q_strid
                  int64_t num_blocks, int32_t block_size, const int32_t* block_table, int64_t bt_rows,
                  int64_t bt_width, const void* slots, int slots_dtype, const void* context_lengths, int ctx_dtype,
                  float sm_scale, void* out, void* workspace, int64_t workspace_bytes, void* stream, int phases,
-                 const NewTokens* fresh);
+                 const NewTokens* fresh, bool use_scratch = false);
 
 }  // namespace
 
@@ -366,6 +405,20 @@ extern "C" int kvfp8_paged_decode_reduce(KVFP8_DECODE_PARAMS) {
     return paged_decode(KVFP8_DECODE_ARGS, kPhaseReduce, nullptr);
 }
 
+// kvfp8_paged_decode with the library's per-device static scratch array as its
+// workspace: no allocation, and sizes whose workspace would not fit are refused.
+extern "C" int kvfp8_paged_decode_noalloc(
+    const void* q, int q_dtype, int64_t q_stride_b, int64_t q_stride_h, int32_t batch, int32_t num_q_heads,
+    int32_t num_kv_heads, int32_t head_dim, const void* k_cache, const void* v_cache, int kv_dtype,
+    const float* k_scales, const float* v_scales, int64_t num_blocks, int32_t block_size,
+    const int32_t* block_table, int64_t bt_rows, int64_t bt_width, const void* slots, int slots_dtype,
+    const void* context_lengths, int ctx_dtype, float sm_scale, void* out, void* stream) {
+    return paged_decode(q, q_dtype, q_stride_b, q_stride_h, batch, num_q_heads, num_kv_heads, head_dim, k_cache,
+                        v_cache, kv_dtype, k_scales, v_scales, num_blocks, block_size, block_table, bt_rows,
+                        bt_width, slots, slots_dtype, context_lengths, ctx_dtype, sm_scale, out, nullptr, 0, stream,
+                        kPhaseSplit | kPhaseReduce, nullptr, true);
+}
+
 extern "C" int kvfp8_append_decode_supported(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
                                              int32_t head_dim, int64_t bt_rows, int64_t bt_width,
                                              int32_t block_size, int kv_dtype) {
@@ -402,7 +455,7 @@ int paged_decode(const void* q, int q_dtype, int64_t q_stride_b, int64_t q_strid
                  int64_t num_blocks, int32_t block_size, const int32_t* block_table, int64_t bt_rows,
                  int64_t bt_width, const void* slots, int slots_dtype, const void* context_lengths, int ctx_dtype,
                  float sm_scale, void* out, void* workspace, int64_t workspace_bytes, void* stream, int phases,
-                 const NewTokens* fresh) {
+                 const NewTokens* fresh, bool use_scratch) {
     if (q_dtype != KVFP8_F32 && q_dtype != KVFP8_F16 && q_dtype != KVFP8_BF16) return KVFP8_EDTYPE;
     if (kv_dtype != KVFP8_E4M3FN && kv_dtype != KVFP8_BF16 && kv_dtype != KVFP8_F16 && kv_dtype != KVFP8_F32)
         return KVFP8_EDTYPE;
@@ -417,10 +470,17 @@ int paged_decode(const void* q, int q_dtype, int64_t q_stride_b, int64_t q_strid
     if (kv_dtype == KVFP8_E4M3FN && (!k_scales || !v_scales)) return KVFP8_ENULL;
 
     const Plan p = make_plan(batch, num_q_heads, num_kv_heads, head_dim, bt_width, block_size, kv_dtype);
-    const int64_t need = workspace_for(p, batch, num_q_heads, num_kv_heads, head_dim);
+    const bool mfma = takes_mfma(p, k_cache, v_cache, bt_rows);
+    const int64_t need = workspace_taken(p, mfma, batch, num_q_heads, num_kv_heads, head_dim);
+    if (use_scratch) {
+        if (need > kScratchBytes) return KVFP8_ELIMIT;
+        const int rc = device_scratch(&workspace);
+        if (rc != KVFP8_OK) return rc;
+        workspace_bytes = kScratchBytes;
+    }
     if (!workspace || workspace_bytes < need) return KVFP8_EWORKSPACE;
     // The fused append runs inside the MFMA kernel over an e4m3fn cache only.
-    if (fresh && (kv_dtype != KVFP8_E4M3FN || !takes_mfma(p, k_cache, v_cache, bt_rows))) return KVFP8_ESHAPE;
+    if (fresh && (kv_dtype != KVFP8_E4M3FN || !mfma)) return KVFP8_ESHAPE;
 
     const int64_t states = (int64_t)batch * p.max_chunks * num_q_heads;
     char* ws = reinterpret_cast<char*>(workspace);

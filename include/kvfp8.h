@@ -167,6 +167,32 @@ int kvfp8_paged_decode_reduce(const void* q_dev, int q_dtype, int64_t q_stride_b
                               void* stream);
 
 /*
+ * kvfp8_paged_decode for callers that cannot allocate device memory: code under HIP
+ * graph capture, serving loops and harnesses that forbid hipMalloc. It has no
+ * counterpart in the reference. Same arguments, computation and results as
+ * kvfp8_paged_decode, bit for bit, minus the workspace: the split-K plan and partial
+ * states live in a static device array of KVFP8_NOALLOC_SCRATCH_BYTES that the
+ * library holds on every device it runs on until the process ends. Shapes whose
+ * workspace would exceed it return KVFP8_ELIMIT before anything is launched. The call
+ * allocates nothing (no hipMalloc/hipFree, no allocating library routine); its first
+ * call on a device looks up that device's array address (hipGetSymbolAddress), so a
+ * caller that captures graphs makes one call on each device before capturing.
+ * Every call on one device uses the same array: calls that overlap on one device
+ * (concurrent streams, or a graph replay concurrent with an eager call) race on it.
+ * Calls ordered on one stream do not.
+ */
+#define KVFP8_NOALLOC_SCRATCH_BYTES (32ll << 20)
+int kvfp8_paged_decode_noalloc(const void* q_dev, int q_dtype, int64_t q_stride_b, int64_t q_stride_h,
+                               int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                               const void* k_cache_dev, const void* v_cache_dev, int kv_dtype,
+                               const float* k_scales_dev, const float* v_scales_dev,
+                               int64_t num_blocks, int32_t block_size,
+                               const int32_t* block_table_dev, int64_t bt_rows, int64_t bt_width,
+                               const void* slots_dev, int slots_dtype,
+                               const void* context_lengths_dev, int ctx_dtype,
+                               float sm_scale, void* out_dev, void* stream);
+
+/*
  * RMSNorm forward over rows of x [rows, d_model] (row stride x_stride elements):
  *   inv_rms[r] = 1 / sqrt(mean_d x[r,d]^2 + eps); out[r,d] = (x[r,d] * inv_rms[r]) * weight[d]
  * in float32, out stored in x's dtype (f32/f16/bf16); weight f32/f16/bf16; inv_rms
