@@ -444,3 +444,30 @@ def test_launches_follow_the_current_stream():
     side.synchronize()
     assert t.equal(got, want)
     assert _native.stream_handle(dev) == t.cuda.current_stream(dev).cuda_stream
+
+
+@t.inference_mode()
+def test_large_batch_with_sixteen_kv_heads():
+    """4,200 sequences x 16 KV heads (two waves per KV head slot of a workgroup): split
+    then reduce equals the single call bit for bit, and sampled rows match the oracle."""
+    from aiproj_amd.kernals.decode_attention import prepare_decode
+
+    batch, hkv, hq, d = 4200, 16, 32, 64
+    lengths = [(i * 37) % 300 + 1 for i in range(batch)]
+    spec = workloads.WorkloadSpec("wide", batch, hq, hkv, d, lengths, seed=16)
+    w = workloads.build(spec, "cuda")
+    cache = PagedKVCache(w.num_blocks, 16, hkv, d, "cuda", FP8)
+    workloads.fill_cache(w, cache, "cuda")
+    k, v = workloads.new_kv(w, "cuda")
+    cache.append_kv(w.new_blocks, w.new_offsets, k, v)
+    ctx = workloads.make_context(w)
+    whole = decode_attention_wrapper(w.q, cache, ctx)
+    call = prepare_decode(w.q, cache, ctx)
+    call.output.fill_(float("nan"))
+    call.split()
+    call.reduce()
+    assert t.equal(call.output.view(t.int16), whole.view(t.int16))
+    rows = [0, 1, 777, batch - 1]
+    expected = oracle_decode(w.q, cache, w.block_table, w.cache_slots, lengths, rows=rows)
+    t.testing.assert_close(whole[rows].double().cpu(), t.from_numpy(expected), rtol=NORTH_STAR_RTOL,
+                           atol=NORTH_STAR_ATOL)
