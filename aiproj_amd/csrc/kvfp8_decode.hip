@@ -33,20 +33,105 @@ constexpr int kMaxBatch = 8191;          // LDS prefix of (batch + 1) int32 <= 3
 constexpr int kGenericChunkTokens = 256;
 constexpr int kMaxGrid = 2048;
 
-template <int KVT> struct KvLoad;
-template <> struct KvLoad<KVFP8_E4M3FN> {
-    static __device__ __forceinline__ float at(const void* p, int64_t i) {
+// Elements of one cache row slice as float32. KvRow<KVT>::load reads `n` elements
+// starting at element e of the cache into x[0 .. n), through 4-byte loads when
+// `dwords` is set (the slice starts on a 4-byte boundary and spans whole dwords),
+// else element by element; x[i] for i >= n is 0.
+template <int KVT> struct KvRow;
+template <> struct KvRow<KVFP8_E4M3FN> {
+    static constexpr int kPerDword = 4;
+    static __device__ __forceinline__ void unpack(uint32_t w, float* x) {
+        // Exact OCP e4m3fn -> float32 conversion, two codes at a time.
+        const auto lo = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w, 1.0f, false);
+        const auto hi = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w, 1.0f, true);
+        x[0] = lo[0];
+        x[1] = lo[1];
+        x[2] = hi[0];
+        x[3] = hi[1];
+    }
+    static __device__ __forceinline__ float one(const void* p, int64_t i) {
         return decode_e4m3fn(reinterpret_cast<const uint8_t*>(p)[i]);
     }
 };
-template <int DT> struct KvLoad {
-    static __device__ __forceinline__ float at(const void* p, int64_t i) {
-        return Elem<DT>::load(reinterpret_cast<const typename Elem<DT>::T*>(p)[i]);
+template <> struct KvRow<KVFP8_BF16> {
+    static constexpr int kPerDword = 2;
+    static __device__ __forceinline__ void unpack(uint32_t w, float* x) {
+        x[0] = __builtin_bit_cast(float, w << 16);
+        x[1] = __builtin_bit_cast(float, w & 0xFFFF0000u);
+    }
+    static __device__ __forceinline__ float one(const void* p, int64_t i) {
+        return bf16_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+    }
+};
+template <> struct KvRow<KVFP8_F16> {
+    static constexpr int kPerDword = 2;
+    static __device__ __forceinline__ void unpack(uint32_t w, float* x) {
+        x[0] = f16_to_f32((uint16_t)(w & 0xFFFFu));
+        x[1] = f16_to_f32((uint16_t)(w >> 16));
+    }
+    static __device__ __forceinline__ float one(const void* p, int64_t i) {
+        return f16_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+    }
+};
+template <> struct KvRow<KVFP8_F32> {
+    static constexpr int kPerDword = 1;
+    static __device__ __forceinline__ void unpack(uint32_t w, float* x) { x[0] = __builtin_bit_cast(float, w); }
+    static __device__ __forceinline__ float one(const void* p, int64_t i) {
+        return reinterpret_cast<const float*>(p)[i];
     }
 };
 
+template <int KVT, int DQ>
+__device__ __forceinline__ void load_slice(const void* cache, int64_t e, int n, float (&x)[DQ]) {
+#pragma unroll
+    for (int i = 0; i < DQ; ++i) x[i] = i < n ? KvRow<KVT>::one(cache, e + i) : 0.0f;
+}
+
+// A lane's slice of one K or V row as raw dwords (n elements from element e; the
+// slice starts on a 4-byte boundary and spans whole dwords), converted at use.
+template <int KVT, int DQ>
+struct RawSlice {
+    static constexpr int kPer = KvRow<KVT>::kPerDword;
+    static constexpr int kW = (DQ + kPer - 1) / kPer;
+    uint32_t w[kW];
+    __device__ __forceinline__ void load(const void* cache, int64_t e, int n) {
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint8_t*>(cache) + e * (4 / kPer));
+#pragma unroll
+        for (int i = 0; i < kW; ++i) w[i] = kPer * i < n ? p[i] : 0u;
+    }
+    __device__ __forceinline__ void clear() {
+#pragma unroll
+        for (int i = 0; i < kW; ++i) w[i] = 0u;
+    }
+    // Element i (a compile-time index after unrolling).
+    template <int I>
+    __device__ __forceinline__ float at() const {
+        float y[kPer];
+        KvRow<KVT>::unpack(w[I / kPer], y);
+        return y[I % kPer];
+    }
+};
+
+template <int KVT, int DQ, int I = 0>
+__device__ __forceinline__ float dot_raw(const RawSlice<KVT, DQ>& r, const float (&q)[DQ]) {
+    if constexpr (I == DQ) return 0.0f;
+    else return q[I] * r.template at<I>() + dot_raw<KVT, DQ, I + 1>(r, q);
+}
+
+template <int KVT, int DQ, int I = 0>
+__device__ __forceinline__ void accumulate_raw(const RawSlice<KVT, DQ>& r, float alpha, float pv, float (&acc)[DQ]) {
+    if constexpr (I < DQ) {
+        acc[I] = acc[I] * alpha + pv * r.template at<I>();
+        accumulate_raw<KVT, DQ, I + 1>(r, alpha, pv, acc);
+    }
+}
+
 // One wave per (sequence, chunk, q head). Lane = (token tok in 0..15, part in
-// 0..3); a lane covers head dims d = part + 4 i, i < DQ (so D <= 4 DQ).
+// 0..3); part p covers the P = ceil(D / 4) contiguous head dims [p P, p P + P)
+// (so D <= 4 DQ). When the rows and the slices are whole dwords
+// (DecodeArgs::kv_dwords) each slice is read with 4-byte loads, and the page-table
+// entry and the K and V slices of the next 16 tokens are loaded while the current
+// ones are used; otherwise element by element.
 template <int KVT, int QT, int DQ>
 __global__ void __launch_bounds__(kDecodeThreads)
 decode_split_generic(DecodeArgs a) {
@@ -59,6 +144,10 @@ decode_split_generic(DecodeArgs a) {
     const int tok = lane >> 2, part = lane & 3;
     const int G = a.num_q_heads / a.num_kv_heads;
     const int D = a.head_dim;
+    const int P = (D + 3) >> 2;
+    const int d0 = part * P;
+    const int nd = max(0, min(P, D - d0));      // dims of this lane
+    const bool dwords = a.kv_dwords != 0;
     const int64_t bs_mask = a.block_size - 1;
     constexpr bool kQuant = KVT == KVFP8_E4M3FN;
 
@@ -79,71 +168,126 @@ decode_split_generic(DecodeArgs a) {
         float qv[DQ], acc[DQ];
 #pragma unroll
         for (int i = 0; i < DQ; ++i) {
-            const int d = part + 4 * i;
-            qv[i] = d < D ? load_q<QT>(a, b, hq, d) * a.score_scale : 0.0f;
+            qv[i] = i < nd ? load_q<QT>(a, b, hq, d0 + i) * a.score_scale : 0.0f;
             acc[i] = 0.0f;
         }
         float m = kNegInf, l = 0.0f;
 
-        for (int64_t base = t0; base < t1; base += 16) {
+        // Cache row of this lane's token in the 16 tokens starting at `base`; valid
+        // false past the chunk or on a page outside the pool.
+        auto row_of = [&](int64_t base, bool& valid) -> int64_t {
             const int64_t t = base + tok;
-            bool valid = t < t1;
+            valid = t < t1;
             int64_t row = 0;
             if (valid) {
                 const int64_t phys = table_row[t >> a.bs_shift];
                 valid = phys >= 0 && phys < a.num_blocks;
                 row = ((phys << a.bs_shift) + (t & bs_mask)) * a.num_kv_heads + h;
-                row = valid ? row : 0;
             }
-            float s = 0.0f;
-            if (valid) {
-#pragma unroll
-                for (int i = 0; i < DQ; ++i) {
-                    const int d = part + 4 * i;
-                    if (d < D) s += qv[i] * KvLoad<KVT>::at(a.k_cache, row * D + d);
-                }
-            }
+            return valid ? row : 0;
+        };
+        // Online softmax per token slot: the four lanes of slot `tok` (tokens tok,
+        // tok + 16, ... of the chunk) keep their own max, sum and accumulators, and
+        // the 16 slots are merged once, after the chunk.
+        auto update = [&](float s, bool valid, float vs, auto&& accumulate) {
             s += __shfl_xor(s, 1);
             s += __shfl_xor(s, 2);
-            float ks = 1.0f, vs = 1.0f;
-            if (kQuant && valid) {
-                ks = a.k_scales[row];
-                vs = a.v_scales[row];
-            }
-            s = valid ? s * ks : kNegInf;
-            float mt = s;
-#pragma unroll
-            for (int off = 4; off < 64; off <<= 1) mt = fmaxf(mt, __shfl_xor(mt, off));
-            const float m_new = fmaxf(m, mt);
-            if (m_new == kNegInf) continue;          // no valid token yet (wave-uniform)
-            const float alpha = exp2f(m - m_new);
-            const float p = valid ? exp2f(s - m_new) : 0.0f;
+            if (!valid) return;
+            const float m_new = fmaxf(m, s);
+            const float m_use = m_new == kNegInf ? 0.0f : m_new;
+            const float alpha = exp2f(m - m_use);       // 0 while m is -inf
+            const float p = exp2f(s - m_use);
             l = l * alpha + p;
-            const float pv = p * vs;
-#pragma unroll
-            for (int i = 0; i < DQ; ++i) {
-                const int d = part + 4 * i;
-                const float v = (valid && d < D) ? KvLoad<KVT>::at(a.v_cache, row * D + d) : 0.0f;
-                acc[i] = acc[i] * alpha + (valid ? pv * v : 0.0f);
-            }
+            accumulate(alpha, p * vs);
             m = m_new;
+        };
+
+        if (dwords) {
+            RawSlice<KVT, DQ> kr, vr;
+            bool valid;
+            int64_t row = row_of(t0, valid);
+            float ks = 1.0f, vs = 1.0f;
+            if (valid) {
+                kr.load(a.k_cache, row * D + d0, nd);
+                vr.load(a.v_cache, row * D + d0, nd);
+                if (kQuant) {
+                    ks = a.k_scales[row];
+                    vs = a.v_scales[row];
+                }
+            } else {
+                kr.clear();
+                vr.clear();
+            }
+            for (int64_t base = t0; base < t1; base += 16) {
+                // The next 16 tokens' loads go out before this group is used.
+                bool nvalid;
+                const int64_t nrow = row_of(base + 16, nvalid);
+                RawSlice<KVT, DQ> nk, nv;
+                float nks = 1.0f, nvs = 1.0f;
+                if (nvalid) {
+                    nk.load(a.k_cache, nrow * D + d0, nd);
+                    nv.load(a.v_cache, nrow * D + d0, nd);
+                    if (kQuant) {
+                        nks = a.k_scales[nrow];
+                        nvs = a.v_scales[nrow];
+                    }
+                } else {
+                    nk.clear();
+                    nv.clear();
+                }
+                const float s = valid ? dot_raw<KVT, DQ>(kr, qv) * ks : 0.0f;
+                update(s, valid, vs, [&](float alpha, float pv) { accumulate_raw<KVT, DQ>(vr, alpha, pv, acc); });
+                kr = nk;
+                vr = nv;
+                ks = nks;
+                vs = nvs;
+                valid = nvalid;
+            }
+        } else {
+            for (int64_t base = t0; base < t1; base += 16) {
+                bool valid;
+                const int64_t row = row_of(base, valid);
+                float s = 0.0f, ks = 1.0f, vs = 1.0f;
+                if (valid) {
+                    float kx[DQ];
+                    load_slice<KVT, DQ>(a.k_cache, row * D + d0, nd, kx);
+#pragma unroll
+                    for (int i = 0; i < DQ; ++i) s += qv[i] * kx[i];
+                    if (kQuant) {
+                        ks = a.k_scales[row];
+                        vs = a.v_scales[row];
+                    }
+                }
+                update(s * ks, valid, vs, [&](float alpha, float pv) {
+                    float vx[DQ];
+                    load_slice<KVT, DQ>(a.v_cache, row * D + d0, nd, vx);
+#pragma unroll
+                    for (int i = 0; i < DQ; ++i) acc[i] = acc[i] * alpha + pv * vx[i];
+                });
+            }
         }
 
+        // Merge the 16 token slots (lanes l and l ^ off, off = 4 .. 32, hold the same
+        // dims of different slots).
 #pragma unroll
         for (int off = 4; off < 64; off <<= 1) {
-            l += __shfl_xor(l, off);
+            const float mo = __shfl_xor(m, off);
+            const float lo = __shfl_xor(l, off);
+            const float mn = fmaxf(m, mo);
+            const float mu = mn == kNegInf ? 0.0f : mn;
+            const float sa = exp2f(m - mu), sb = exp2f(mo - mu);
+            l = l * sa + lo * sb;
 #pragma unroll
-            for (int i = 0; i < DQ; ++i) acc[i] += __shfl_xor(acc[i], off);
+            for (int i = 0; i < DQ; ++i) acc[i] = acc[i] * sa + __shfl_xor(acc[i], off) * sb;
+            m = mn;
         }
 
         if (nchunks == 1) {
             if (tok == 0) {
                 const float inv = l > 0.0f ? 1.0f / l : 0.0f;
 #pragma unroll
-                for (int i = 0; i < DQ; ++i) {
-                    const int d = part + 4 * i;
-                    if (d < D) store_out<QT>(a, b, hq, d, l > 0.0f ? acc[i] * inv : 0.0f);
-                }
+                for (int i = 0; i < DQ; ++i)
+                    if (i < nd) store_out<QT>(a, b, hq, d0 + i, l > 0.0f ? acc[i] * inv : 0.0f);
             }
         } else {
             const int64_t pi = part_index(a, b, c, hq);
@@ -153,10 +297,8 @@ decode_split_generic(DecodeArgs a) {
             }
             if (tok == 0) {
 #pragma unroll
-                for (int i = 0; i < DQ; ++i) {
-                    const int d = part + 4 * i;
-                    if (d < D) a.part_acc[pi * D + d] = acc[i];
-                }
+                for (int i = 0; i < DQ; ++i)
+                    if (i < nd) a.part_acc[pi * D + d0 + i] = acc[i];
             }
         }
     }
@@ -513,6 +655,14 @@ int paged_decode(const void* q, int q_dtype, int64_t q_stride_b, int64_t q_strid
     a.part_acc = reinterpret_cast<float*>(ws + 2 * align256(states * sizeof(float)));
     a.chunk_tokens = p.chunk_tokens;
     a.max_chunks = p.max_chunks;
+    {
+        // Dword slices: each lane's P = D / 4 dims are whole dwords (D a multiple of
+        // 4 elements per dword x 4 parts) and the caches are 4-byte aligned.
+        const int esize = kv_dtype == KVFP8_E4M3FN ? 1 : kv_dtype == KVFP8_F32 ? 4 : 2;
+        const int per_dword = 4 / esize;
+        const bool aligned = (((uintptr_t)k_cache | (uintptr_t)v_cache) & 3) == 0;
+        a.kv_dwords = aligned && head_dim % (4 * per_dword) == 0 ? 1 : 0;
+    }
     a.new_k = fresh ? fresh->k : nullptr;
     a.new_v = fresh ? fresh->v : nullptr;
     a.new_dtype = fresh ? fresh->dtype : KVFP8_BF16;

@@ -424,9 +424,9 @@ def _time_decode(caches, q, context, steps: int):
 
 
 def _misaligned(cache):
-    """The same cache with its K and V codes copied one byte past a 16-byte boundary:
+    """The same cache with its K and V codes copied 4 bytes past a 16-byte boundary:
     the MFMA kernel needs 16-byte aligned caches, so decode takes the generic VALU
-    kernel on identical bytes (scales and table unchanged)."""
+    kernel (with its 4-byte loads) on identical bytes (scales and table unchanged)."""
     import types
 
     import torch as t
@@ -434,7 +434,7 @@ def _misaligned(cache):
     def shifted(x):
         nbytes = x.numel() * x.element_size()
         raw = t.empty(nbytes + 16, dtype=t.uint8, device=x.device)
-        view = raw[1:1 + nbytes].view(x.dtype).view(x.shape)
+        view = raw[4:4 + nbytes].view(x.dtype).view(x.shape)
         view.view(t.uint8).copy_(x.view(t.uint8))
         return view
 
