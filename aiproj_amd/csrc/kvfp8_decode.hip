@@ -304,6 +304,292 @@ decode_split_generic(DecodeArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Grouped VALU kernel: one wave per (sequence, chunk, KV head, group of q heads),
+// so each K/V row is read once for every q head of its group.
+// ---------------------------------------------------------------------------
+
+// DPP lane permutations within rows of 16 lanes.
+constexpr int kDppXor1 = 0xB1;          // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4E;          // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141;   // lane i <-> 7 - i within each 8 lanes
+constexpr int kDppMirror = 0x140;       // lane i <-> 15 - i within each row
+constexpr int kDppRor4 = 0x124;         // rotate each row by 4 lanes
+constexpr int kDppRor8 = 0x128;         // rotate each row by 8 lanes
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over lanes l, l ^ 16, l ^ 32 and l ^ 48, through ds_bpermute. (A
+// v_permlane16/32_swap of a value with itself would do it without the LDS
+// crossbar, but this compiler's optimizer folds an operation on the two results
+// of such a swap into an operation on the first result twice.)
+__device__ __forceinline__ float sum_rows4(float x) {
+    x += __shfl_xor(x, 16);
+    return x + __shfl_xor(x, 32);
+}
+
+// Sum over the `parts` consecutive lanes of one token (parts = 4, 8 or 16); every
+// one of them receives the same value (each step adds a commuted pair).
+__device__ __forceinline__ float sum_parts(float x, int parts) {
+    x += dpp<kDppXor1>(x);
+    x += dpp<kDppXor2>(x);
+    if (parts >= 8) x += dpp<kDppHalfMirror>(x);
+    if (parts >= 16) x += dpp<kDppMirror>(x);
+    return x;
+}
+
+// Sum over the lanes holding the same part of different tokens (lane = token x
+// parts + part); every lane receives its part's total.
+__device__ __forceinline__ float sum_tokens(float x, int parts) {
+    if (parts == 4) x += dpp<kDppRor4>(x);
+    if (parts <= 8) x += dpp<kDppRor8>(x);
+    return sum_rows4(x);
+}
+
+// Maximum over the wave: each row's maximum in all its lanes, then the four rows'
+// values read into scalar registers.
+__device__ __forceinline__ float wave_max(float x) {
+    x = fmaxf(x, dpp<kDppXor1>(x));
+    x = fmaxf(x, dpp<kDppXor2>(x));
+    x = fmaxf(x, dpp<kDppHalfMirror>(x));
+    x = fmaxf(x, dpp<kDppMirror>(x));
+    const int u = __builtin_bit_cast(int, x);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(u, 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(u, 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(u, 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(u, 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+__device__ __forceinline__ float load_q_any(const DecodeArgs& a, int b, int hq, int d) {
+    const int64_t i = (int64_t)b * a.q_stride_b + (int64_t)hq * a.q_stride_h + d;
+    if (a.q_dtype == KVFP8_F32) return reinterpret_cast<const float*>(a.q)[i];
+    const uint16_t h = reinterpret_cast<const uint16_t*>(a.q)[i];
+    return a.q_dtype == KVFP8_F16 ? f16_to_f32(h) : bf16_to_f32(h);
+}
+
+__device__ __forceinline__ void store_out_any(const DecodeArgs& a, int b, int hq, int d, float x) {
+    const int64_t i = ((int64_t)b * a.num_q_heads + hq) * a.head_dim + d;
+    if (a.q_dtype == KVFP8_F32) reinterpret_cast<float*>(a.out)[i] = x;
+    else if (a.q_dtype == KVFP8_F16) reinterpret_cast<uint16_t*>(a.out)[i] = f32_to_f16(x);
+    else reinterpret_cast<uint16_t*>(a.out)[i] = f32_to_bf16(x);
+}
+
+// A lane's P elements of one K or V row, read with unconditional 4-byte-aligned
+// loads (which the compiler merges into 16-byte loads).
+template <int KVT, int P>
+struct RowSlice {
+    static constexpr int kPer = KvRow<KVT>::kPerDword;
+    static constexpr int kW = P / kPer;
+    static_assert(P % kPer == 0, "a slice spans whole dwords");
+    uint32_t w[kW];
+    __device__ __forceinline__ void load(const void* cache, int64_t e) {
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint8_t*>(cache) + e * (4 / kPer));
+#pragma unroll
+        for (int i = 0; i < kW; ++i) w[i] = p[i];
+    }
+    __device__ __forceinline__ void clear() {
+#pragma unroll
+        for (int i = 0; i < kW; ++i) w[i] = 0u;
+    }
+    __device__ __forceinline__ void unpack(float (&x)[P]) const {
+#pragma unroll
+        for (int i = 0; i < kW; ++i) KvRow<KVT>::unpack(w[i], x + i * kPer);
+    }
+};
+
+// q heads per work unit: as many as keep q, the accumulators and two stages of
+// K/V slices within 256 registers (two waves per SIMD).
+template <int KVT, int P>
+constexpr int grouped_heads() {
+    constexpr int stage = 2 * P / KvRow<KVT>::kPerDword;
+    return 2 * 4 * P + 2 * stage + P + 40 <= 250 ? 4 : 2;
+}
+
+constexpr int kGroupPages = 256;   // page-list entries per wave: one chunk at page size 1
+static_assert(kGenericChunkTokens <= kGroupPages, "a chunk's page list fits the wave's LDS region");
+constexpr float kRescaleLog2 = 8.0f;  // the reference max moves when a score exceeds it by 2^8
+
+// One wave per (sequence, chunk, KV head, group of `group_heads` q heads).
+// Lane = (token tok, part): parts = D / P lanes share a token, part p holding the
+// contiguous dims [p P, p P + P) of its K and V rows for every q head of the
+// group; a step covers 64 / parts tokens. The page-table entries of the chunk are
+// staged once into the wave's LDS region; the next step's K/V slices load while
+// the current ones are used.
+// Softmax: a wave-uniform reference max per head that moves only when some score
+// exceeds it by 2^8 (then the accumulators are rescaled); each token's probability
+// is exp2(s - max) <= 256. The token slots are summed once, after the chunk.
+template <int KVT, int P>
+__global__ void __launch_bounds__(kDecodeThreads) __attribute__((amdgpu_waves_per_eu(2)))
+decode_split_grouped(DecodeArgs a) {
+    extern __shared__ int32_t prefix[];
+    build_chunk_prefix<kDecodeThreads>(a, prefix);
+    constexpr int kGH = grouped_heads<KVT, P>();
+    constexpr bool kQuant = KVT == KVFP8_E4M3FN;
+    using Slice = RowSlice<KVT, P>;
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    int32_t* pages = prefix + ((a.batch + 4) & ~3) + wave * kGroupPages;
+    const int D = a.head_dim;
+    const int parts = D / P;                                   // 4, 8 or 16
+    const int pshift = parts == 4 ? 2 : (parts == 8 ? 3 : 4);
+    const int tok = lane >> pshift, part = lane & (parts - 1);
+    const int step = 64 >> pshift;
+    const int d0 = part * P;
+    const int G = a.num_q_heads / a.num_kv_heads;
+    const int gh = a.group_heads;
+    const int ngroups = (G + gh - 1) / gh;
+    const int U = a.num_kv_heads * ngroups;
+    const int64_t total = (int64_t)prefix[a.batch] * U;
+    const int64_t bs_mask = a.block_size - 1;
+
+    for (int64_t w = (int64_t)blockIdx.x * kWavesPerBlock + wave; w < total;
+         w += (int64_t)gridDim.x * kWavesPerBlock) {
+        const int32_t chunk = (int32_t)(w / U);
+        const int r = (int)(w - (int64_t)chunk * U);
+        const int h = r / ngroups, grp = r - h * ngroups;
+        const int hq0 = h * G + grp * gh;
+        const int nh = min(gh, G - grp * gh);
+        const int b = find_seq(prefix, a.batch, chunk);
+        const int c = chunk - prefix[b];
+        const int nchunks = prefix[b + 1] - prefix[b];
+        int64_t slot;
+        const int64_t len = seq_tokens(a, b, &slot);
+        const int64_t t0 = (int64_t)c * a.chunk_tokens;
+        const int64_t t1 = min(t0 + (int64_t)a.chunk_tokens, len);
+        const int32_t* table_row = a.block_table + slot * a.bt_width;
+        const int64_t first_page = t0 >> a.bs_shift;
+        const int npages = (int)(((t1 - 1) >> a.bs_shift) - first_page + 1);
+        // LDS accesses of one wave complete in order: the reads below see these
+        // writes, and the previous unit's reads are done before they land.
+        for (int i = lane; i < npages; i += 64) pages[i] = table_row[first_page + i];
+
+        float qv[kGH][P], acc[kGH][P], m[kGH], l[kGH];
+#pragma unroll
+        for (int g = 0; g < kGH; ++g) {
+            const int hq = hq0 + min(g, nh - 1);
+#pragma unroll
+            for (int e = 0; e < P; ++e) {
+                qv[g][e] = load_q_any(a, b, hq, d0 + e) * a.score_scale;
+                acc[g][e] = 0.0f;
+            }
+            m[g] = kNegInf;
+            l[g] = 0.0f;
+        }
+
+        // K/V slices and scales of this lane's token in the step at `base`; false
+        // (and zeros) past the chunk or on a page outside the pool.
+        auto fetch = [&](int64_t base, Slice& kr, Slice& vr, float& ks, float& vs) __attribute__((always_inline)) {
+            const int64_t t = base + tok;
+            bool valid = t < t1;
+            if (valid) {
+                const int64_t phys = pages[(int)((t >> a.bs_shift) - first_page)];
+                valid = phys >= 0 && phys < a.num_blocks;
+                if (valid) {
+                    const int64_t row = ((phys << a.bs_shift) + (t & bs_mask)) * a.num_kv_heads + h;
+                    kr.load(a.k_cache, row * D + d0);
+                    vr.load(a.v_cache, row * D + d0);
+                    if (kQuant) {
+                        ks = a.k_scales[row];
+                        vs = a.v_scales[row];
+                    }
+                }
+            }
+            if (!valid) {
+                kr.clear();
+                vr.clear();
+                ks = 0.0f;
+                vs = 0.0f;
+            }
+            return valid;
+        };
+
+        Slice kr, vr;
+        float ks = 1.0f, vs = 1.0f;
+        bool valid = fetch(t0, kr, vr, ks, vs);
+        for (int64_t base = t0; base < t1; base += step) {
+            Slice nk, nv;
+            float nks = 1.0f, nvs = 1.0f;
+            const bool nvalid = fetch(base + step, nk, nv, nks, nvs);
+
+            float kx[P];
+            kr.unpack(kx);
+            float s[kGH];
+            bool need = false;
+#pragma unroll
+            for (int g = 0; g < kGH; ++g) {
+                float x = 0.0f;
+#pragma unroll
+                for (int e = 0; e < P; ++e) x += qv[g][e] * kx[e];
+                s[g] = valid ? sum_parts(x, parts) * ks : kNegInf;
+                need |= valid && s[g] > m[g] + kRescaleLog2;
+            }
+            if (__any(need)) {
+#pragma unroll
+                for (int g = 0; g < kGH; ++g) {
+                    const float mn = fmaxf(m[g], wave_max(s[g]));
+                    const float alpha = m[g] == kNegInf ? 0.0f : exp2f(m[g] - mn);
+                    l[g] *= alpha;
+#pragma unroll
+                    for (int e = 0; e < P; ++e) acc[g][e] *= alpha;
+                    m[g] = mn;
+                }
+            }
+            float vx[P];
+            vr.unpack(vx);
+#pragma unroll
+            for (int g = 0; g < kGH; ++g) {
+                const float p = valid ? exp2f(s[g] - m[g]) : 0.0f;
+                l[g] += p;
+                const float pv = p * vs;
+#pragma unroll
+                for (int e = 0; e < P; ++e) acc[g][e] += pv * vx[e];
+            }
+            kr = nk;
+            vr = nv;
+            ks = nks;
+            vs = nvs;
+            valid = nvalid;
+        }
+
+        // Sum the token slots; lanes tok == 0 write their part's dims.
+#pragma unroll
+        for (int g = 0; g < kGH; ++g) {
+            l[g] = sum_tokens(l[g], parts);
+#pragma unroll
+            for (int e = 0; e < P; ++e) acc[g][e] = sum_tokens(acc[g][e], parts);
+        }
+        if (nchunks == 1) {
+            if (tok == 0) {
+#pragma unroll
+                for (int g = 0; g < kGH; ++g) {
+                    if (g >= nh) break;
+                    const float inv = l[g] > 0.0f ? 1.0f / l[g] : 0.0f;
+#pragma unroll
+                    for (int e = 0; e < P; ++e) store_out_any(a, b, hq0 + g, d0 + e, l[g] > 0.0f ? acc[g][e] * inv : 0.0f);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int g = 0; g < kGH; ++g) {
+                if (g >= nh) break;
+                const int64_t pi = part_index(a, b, c, hq0 + g);
+                if (lane == 0) {
+                    a.part_m[pi] = m[g];
+                    a.part_l[pi] = l[g];
+                }
+                if (tok == 0) {
+#pragma unroll
+                    for (int e = 0; e < P; ++e) a.part_acc[pi * D + d0 + e] = acc[g][e];
+                }
+            }
+        }
+    }
+}
+
 // Merge of split-K partials, reference decode_attention.py:437-550:
 //   M = max_c m_c; den = sum_c 2^(m_c - M) l_c; num = sum_c 2^(m_c - M) acc_c
 //   out = den > 0 ? num / den : 0
@@ -448,6 +734,42 @@ hipError_t launch_generic(const DecodeArgs& a, int64_t units_total, hipStream_t 
     return launch_timed(decode_split_generic<KVT, QT, 128>, grid, block, lds, s, timing, a);
 }
 
+// Slice width P of the grouped kernel for head size d, or 0 when it does not take
+// the shape: d = parts x P with parts in {4, 8, 16} and P in {4, 8, 16, 20}.
+int grouped_slice(int d) {
+    for (int parts = 4; parts <= 16; parts *= 2) {
+        if (d % parts != 0) continue;
+        const int p = d / parts;
+        if (p == 4 || p == 8 || p == 16 || p == 20) return p;
+    }
+    return 0;
+}
+
+template <int KVT, int P>
+hipError_t launch_grouped_p(DecodeArgs a, const Plan& p, hipStream_t s) {
+    constexpr int kGH = grouped_heads<KVT, P>();
+    const int G = a.num_q_heads / a.num_kv_heads;
+    const int ngroups = (G + kGH - 1) / kGH;
+    a.group_heads = (G + ngroups - 1) / ngroups;          // balanced groups of at most kGH heads
+    const int64_t units = (int64_t)a.batch * p.max_chunks * a.num_kv_heads * ngroups;
+    const size_t lds = (size_t)((a.batch + 4) & ~3) * sizeof(int32_t) +
+                       (size_t)kWavesPerBlock * kGroupPages * sizeof(int32_t);
+    int64_t blocks = (units + kWavesPerBlock - 1) / kWavesPerBlock;
+    blocks = blocks < 1 ? 1 : (blocks > kMaxGrid ? kMaxGrid : blocks);
+    return launch_timed(decode_split_grouped<KVT, P>, dim3((unsigned)blocks), dim3(kDecodeThreads), lds, s,
+                        next_kernel_timing(), a);
+}
+
+template <int KVT>
+hipError_t launch_grouped(const DecodeArgs& a, int slice, const Plan& p, hipStream_t s) {
+    switch (slice) {
+        case 4: return launch_grouped_p<KVT, 4>(a, p, s);
+        case 8: return launch_grouped_p<KVT, 8>(a, p, s);
+        case 16: return launch_grouped_p<KVT, 16>(a, p, s);
+        default: return launch_grouped_p<KVT, 20>(a, p, s);
+    }
+}
+
 template <int QT>
 hipError_t launch_combine(const DecodeArgs& a, hipStream_t s) {
     const int64_t pairs = (int64_t)a.batch * a.num_q_heads;
@@ -488,8 +810,19 @@ hipError_t dispatch_kv(const DecodeArgs& a, int kv_dtype, const Plan& p, void* w
         return launch_mfma_decode<QT>(a, kv_dtype, workspace, s, phases);
     if (phases & kPhaseSplit) {
         const int64_t units_total = (int64_t)a.batch * p.max_chunks * a.num_q_heads;
+        // The grouped kernel reads whole dwords: 4-byte aligned caches, and a head
+        // size it splits into slices.
+        const bool aligned4 = (((uintptr_t)a.k_cache | (uintptr_t)a.v_cache) & 3) == 0;
+        const int slice = aligned4 ? grouped_slice(a.head_dim) : 0;
         hipError_t err;
-        switch (kv_dtype) {
+        if (slice != 0) {
+            switch (kv_dtype) {
+                case KVFP8_E4M3FN: err = launch_grouped<KVFP8_E4M3FN>(a, slice, p, s); break;
+                case KVFP8_BF16: err = launch_grouped<KVFP8_BF16>(a, slice, p, s); break;
+                case KVFP8_F16: err = launch_grouped<KVFP8_F16>(a, slice, p, s); break;
+                default: err = launch_grouped<KVFP8_F32>(a, slice, p, s); break;
+            }
+        } else switch (kv_dtype) {
             case KVFP8_E4M3FN: err = launch_generic<KVFP8_E4M3FN, QT>(a, units_total, s); break;
             case KVFP8_BF16: err = launch_generic<KVFP8_BF16, QT>(a, units_total, s); break;
             case KVFP8_F16: err = launch_generic<KVFP8_F16, QT>(a, units_total, s); break;
@@ -663,6 +996,8 @@ int paged_decode(const void* q, int q_dtype, int64_t q_stride_b, int64_t q_strid
         const bool aligned = (((uintptr_t)k_cache | (uintptr_t)v_cache) & 3) == 0;
         a.kv_dwords = aligned && head_dim % (4 * per_dword) == 0 ? 1 : 0;
     }
+    a.q_dtype = q_dtype;
+    a.group_heads = 1;
     a.new_k = fresh ? fresh->k : nullptr;
     a.new_v = fresh ? fresh->v : nullptr;
     a.new_dtype = fresh ? fresh->dtype : KVFP8_BF16;

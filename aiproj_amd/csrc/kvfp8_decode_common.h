@@ -44,6 +44,8 @@ struct DecodeArgs {
     int32_t chunk_tokens;     // tokens per work item (a multiple of 16)
     int32_t max_chunks;       // ceil(bt_width * block_size / chunk_tokens)
     int32_t kv_dwords;        // generic kernel: a lane's slice of a K/V row is read as whole dwords
+    int32_t q_dtype;          // grouped kernel: element type of q and out (kvfp8_dtype)
+    int32_t group_heads;      // grouped kernel: q heads per work unit (of one KV head's group)
     // Fused append (kvfp8_append_paged_decode): the new token of every sequence,
     // rows [batch, Hkv, D] with element strides (row stride, D, 1), quantized into
     // the cache at (new_blocks[b], new_offsets[b]), the sequence's last attended

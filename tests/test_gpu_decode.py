@@ -208,7 +208,9 @@ def test_decode_edge_cases_and_calling_forms():
 
 @t.inference_mode()
 def test_decode_block_sizes_other_than_16():
-    for block_size in (4, 8, 32, 64):
+    # Page sizes under 16 take the VALU kernel; 1 and 2 fill its whole per-wave
+    # page list (256 entries for a 256-token chunk).
+    for block_size in (1, 2, 4, 8, 32, 64):
         lengths = [3, 40, 129]
         cache = PagedKVCache(sum(-(-n // block_size) for n in lengths) + 4, block_size, 2, 64, "cuda", FP8)
         manager, context, _, _ = fill_decode_batch([cache], lengths, 2, 64, block_size, t.bfloat16, seed=10)
@@ -216,6 +218,58 @@ def test_decode_block_sizes_other_than_16():
         out = decode_attention_wrapper(q, cache, context)
         expected = oracle_decode(q, cache, manager.block_table, context.cache_slots, lengths)
         t.testing.assert_close(out.double().cpu(), t.from_numpy(expected), rtol=1e-4, atol=1e-4)
+
+
+def _shifted(x, offset):
+    """x's bytes copied `offset` bytes past a 16-byte boundary (same shape and dtype)."""
+    nbytes = x.numel() * x.element_size()
+    raw = t.empty(nbytes + 16, dtype=t.uint8, device=x.device)
+    view = raw[offset:offset + nbytes].view(x.dtype).view(x.shape)
+    view.view(t.uint8).copy_(x.view(t.uint8))
+    return view
+
+
+@t.inference_mode()
+@pytest.mark.parametrize("offset", [4, 1])
+@pytest.mark.parametrize("cache_dtype,q_dtype", [(FP8, t.bfloat16), (FP8, t.float32), (t.bfloat16, t.bfloat16),
+                                                 (t.float16, t.float16), (t.float32, t.float32)])
+def test_unaligned_caches_take_the_valu_kernels(offset, cache_dtype, q_dtype):
+    # The MFMA kernel needs 16-byte aligned caches. 4-byte aligned caches take the
+    # grouped VALU kernel (whole-dword slices), byte-aligned ones the per-element
+    # path; both against the oracle on the same bytes, at the north-star head
+    # layout (32q/8kv, D 128) with lengths across chunk boundaries.
+    esize = t.empty((), dtype=cache_dtype).element_size()
+    if offset % esize:
+        pytest.skip("a cache tensor starts on a multiple of its element size")
+    lengths = [1, 17, 256, 257, 700, 1300]
+    hq, hkv, d = 32, 8, 128
+    cache = PagedKVCache(sum(-(-n // 16) for n in lengths) + 4, 16, hkv, d, "cuda", cache_dtype)
+    manager, context, _, _ = fill_decode_batch([cache], lengths, hkv, d, 16, t.bfloat16, seed=16)
+    q = t.randn(len(lengths), hq, d, device="cuda").to(q_dtype)
+    read = PagedKVRead(_shifted(cache.k, offset), _shifted(cache.v, offset), cache.k_scales, cache.v_scales,
+                       manager.block_table, context.cache_slots, context.context_lengths, 16)
+    actual = decode_attention_wrapper(q, read)
+    expected = oracle_decode(q, cache, manager.block_table, context.cache_slots, lengths)
+    tol = OUTPUT_TOLERANCE[q_dtype]
+    t.testing.assert_close(actual.double().cpu(), t.from_numpy(expected), rtol=tol, atol=tol)
+    # Identical to the aligned call within the same tolerance (MFMA or grouped kernel).
+    aligned = decode_attention_wrapper(q, cache, context)
+    t.testing.assert_close(actual.double().cpu(), aligned.double().cpu(), rtol=2 * tol, atol=2 * tol)
+
+
+@t.inference_mode()
+@pytest.mark.parametrize("num_q_heads,num_kv_heads", [(32, 1), (12, 2), (6, 6)])
+def test_valu_kernel_head_groups(num_q_heads, num_kv_heads):
+    # D 80 (no MFMA kernel): groups of 32, 6 and 1 q heads per KV head, which the
+    # grouped kernel splits into balanced sets of at most four heads per wave.
+    lengths = [2, 33, 300, 900]
+    d = 80
+    cache = PagedKVCache(sum(-(-n // 16) for n in lengths) + 4, 16, num_kv_heads, d, "cuda", FP8)
+    manager, context, _, _ = fill_decode_batch([cache], lengths, num_kv_heads, d, 16, t.bfloat16, seed=17)
+    q = t.randn(len(lengths), num_q_heads, d, device="cuda", dtype=t.float32)
+    actual = decode_attention_wrapper(q, cache, context)
+    expected = oracle_decode(q, cache, manager.block_table, context.cache_slots, lengths)
+    t.testing.assert_close(actual.double().cpu(), t.from_numpy(expected), rtol=1e-4, atol=1e-4)
 
 
 @t.inference_mode()
