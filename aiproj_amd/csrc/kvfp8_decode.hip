@@ -319,7 +319,8 @@ constexpr int kDppRor8 = 0x128;         // rotate each row by 8 lanes
 
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+    return __builtin_bit_cast(float,
+                              __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
 }
 
 // Sum over lanes l, l ^ 16, l ^ 32 and l ^ 48, through ds_bpermute. (A
@@ -364,18 +365,51 @@ __device__ __forceinline__ float wave_max(float x) {
     return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
-__device__ __forceinline__ float load_q_any(const DecodeArgs& a, int b, int hq, int d) {
-    const int64_t i = (int64_t)b * a.q_stride_b + (int64_t)hq * a.q_stride_h + d;
-    if (a.q_dtype == KVFP8_F32) return reinterpret_cast<const float*>(a.q)[i];
-    const uint16_t h = reinterpret_cast<const uint16_t*>(a.q)[i];
-    return a.q_dtype == KVFP8_F16 ? f16_to_f32(h) : bf16_to_f32(h);
+// q rows hq0 + g (g < KG; rows past nh repeat row nh - 1), elements d0 .. d0 + P,
+// times `scale`. One branch on the q dtype around all the loads, so that they are
+// in flight together.
+template <int KG, int P>
+__device__ __forceinline__ void load_q_group(const DecodeArgs& a, int b, int hq0, int nh, int d0, float scale,
+                                             float (&x)[KG][P]) {
+    int64_t row[KG];
+#pragma unroll
+    for (int g = 0; g < KG; ++g)
+        row[g] = (int64_t)b * a.q_stride_b + (int64_t)(hq0 + min(g, nh - 1)) * a.q_stride_h + d0;
+    if (a.q_dtype == KVFP8_F32) {
+        const float* q = reinterpret_cast<const float*>(a.q);
+#pragma unroll
+        for (int g = 0; g < KG; ++g)
+#pragma unroll
+            for (int e = 0; e < P; ++e) x[g][e] = q[row[g] + e] * scale;
+    } else {
+        const uint16_t* q = reinterpret_cast<const uint16_t*>(a.q);
+        uint16_t h[KG][P];
+#pragma unroll
+        for (int g = 0; g < KG; ++g)
+#pragma unroll
+            for (int e = 0; e < P; ++e) h[g][e] = q[row[g] + e];
+        const bool f16 = a.q_dtype == KVFP8_F16;
+#pragma unroll
+        for (int g = 0; g < KG; ++g)
+#pragma unroll
+            for (int e = 0; e < P; ++e) x[g][e] = (f16 ? f16_to_f32(h[g][e]) : bf16_to_f32(h[g][e])) * scale;
+    }
 }
 
-__device__ __forceinline__ void store_out_any(const DecodeArgs& a, int b, int hq, int d, float x) {
-    const int64_t i = ((int64_t)b * a.num_q_heads + hq) * a.head_dim + d;
-    if (a.q_dtype == KVFP8_F32) reinterpret_cast<float*>(a.out)[i] = x;
-    else if (a.q_dtype == KVFP8_F16) reinterpret_cast<uint16_t*>(a.out)[i] = f32_to_f16(x);
-    else reinterpret_cast<uint16_t*>(a.out)[i] = f32_to_bf16(x);
+// out[b, hq, d0 .. d0 + P) = x, converted to the q dtype (one branch).
+template <int P>
+__device__ __forceinline__ void store_out_row(const DecodeArgs& a, int b, int hq, int d0, const float (&x)[P]) {
+    const int64_t i0 = ((int64_t)b * a.num_q_heads + hq) * a.head_dim + d0;
+    if (a.q_dtype == KVFP8_F32) {
+#pragma unroll
+        for (int e = 0; e < P; ++e) reinterpret_cast<float*>(a.out)[i0 + e] = x[e];
+    } else if (a.q_dtype == KVFP8_F16) {
+#pragma unroll
+        for (int e = 0; e < P; ++e) reinterpret_cast<uint16_t*>(a.out)[i0 + e] = f32_to_f16(x[e]);
+    } else {
+#pragma unroll
+        for (int e = 0; e < P; ++e) reinterpret_cast<uint16_t*>(a.out)[i0 + e] = f32_to_bf16(x[e]);
+    }
 }
 
 // A lane's P elements of one K or V row, read with unconditional 4-byte-aligned
@@ -401,12 +435,27 @@ struct RowSlice {
     }
 };
 
-// q heads per work unit: as many as keep q, the accumulators and two stages of
-// K/V slices within 256 registers (two waves per SIMD).
+// Register plan of the grouped kernel: q and the accumulators take 2 x heads x P
+// registers, each stage of K/V slices and scales 2 P / (elements per dword) + 3.
+// Both stay within 190 of the 256 registers of two waves per SIMD (a budget
+// measured on the compiled kernels: the rest hold addresses, unpacked slices and
+// softmax state). Heads come first (up to 4: each K/V row is then read once for
+// four q heads), then three stages (loads two steps ahead) where they fit, else two.
+template <int KVT, int P>
+struct GroupedPlan {
+    static constexpr int kStage = 2 * P / KvRow<KVT>::kPerDword + 3;
+    static constexpr int heads() {
+        for (int h = 4; h > 1; --h)
+            if (2 * h * P + 2 * kStage <= 190) return h;
+        return 1;
+    }
+    static constexpr int kHeads = heads();
+    static constexpr int kStages = 2 * kHeads * P + 3 * kStage <= 190 ? 3 : 2;
+};
+
 template <int KVT, int P>
 constexpr int grouped_heads() {
-    constexpr int stage = 2 * P / KvRow<KVT>::kPerDword;
-    return 2 * 4 * P + 2 * stage + P + 40 <= 250 ? 4 : 2;
+    return GroupedPlan<KVT, P>::kHeads;
 }
 
 constexpr int kGroupPages = 256;   // page-list entries per wave: one chunk at page size 1
@@ -468,91 +517,120 @@ decode_split_grouped(DecodeArgs a) {
         for (int i = lane; i < npages; i += 64) pages[i] = table_row[first_page + i];
 
         float qv[kGH][P], acc[kGH][P], m[kGH], l[kGH];
+        load_q_group<kGH, P>(a, b, hq0, nh, d0, a.score_scale, qv);
 #pragma unroll
         for (int g = 0; g < kGH; ++g) {
-            const int hq = hq0 + min(g, nh - 1);
 #pragma unroll
-            for (int e = 0; e < P; ++e) {
-                qv[g][e] = load_q_any(a, b, hq, d0 + e) * a.score_scale;
-                acc[g][e] = 0.0f;
-            }
+            for (int e = 0; e < P; ++e) acc[g][e] = 0.0f;
             m[g] = kNegInf;
             l[g] = 0.0f;
         }
 
-        // K/V slices and scales of this lane's token in the step at `base`; false
-        // (and zeros) past the chunk or on a page outside the pool.
-        auto fetch = [&](int64_t base, Slice& kr, Slice& vr, float& ks, float& vs) __attribute__((always_inline)) {
+        // One step's K/V slices and scales in registers.
+        struct Stage {
+            Slice k, v;
+            float ks, vs;
+            bool valid;
+        };
+        // Loads of the step at `base` for this lane's token. The loads are
+        // unconditional, so that the compiler counts them exactly and waits for each
+        // stage alone: a lane whose token lies past the chunk or on a page outside
+        // the pool reads row 0 of the pool instead and is marked invalid; `use`
+        // ignores its K and zeroes its V and V scale.
+        auto fetch = [&](int64_t base, Stage& st) __attribute__((always_inline)) {
             const int64_t t = base + tok;
             bool valid = t < t1;
+            int64_t row = 0;
             if (valid) {
                 const int64_t phys = pages[(int)((t >> a.bs_shift) - first_page)];
                 valid = phys >= 0 && phys < a.num_blocks;
-                if (valid) {
-                    const int64_t row = ((phys << a.bs_shift) + (t & bs_mask)) * a.num_kv_heads + h;
-                    kr.load(a.k_cache, row * D + d0);
-                    vr.load(a.v_cache, row * D + d0);
-                    if (kQuant) {
-                        ks = a.k_scales[row];
-                        vs = a.v_scales[row];
-                    }
-                }
+                row = valid ? ((phys << a.bs_shift) + (t & bs_mask)) * a.num_kv_heads + h : 0;
             }
-            if (!valid) {
-                kr.clear();
-                vr.clear();
-                ks = 0.0f;
-                vs = 0.0f;
+            st.k.load(a.k_cache, row * D + d0);
+            st.v.load(a.v_cache, row * D + d0);
+            if (kQuant) {
+                st.ks = a.k_scales[row];
+                st.vs = a.v_scales[row];
+            } else {
+                st.ks = 1.0f;
+                st.vs = 1.0f;
             }
-            return valid;
+            st.valid = valid;
         };
-
-        Slice kr, vr;
-        float ks = 1.0f, vs = 1.0f;
-        bool valid = fetch(t0, kr, vr, ks, vs);
-        for (int64_t base = t0; base < t1; base += step) {
-            Slice nk, nv;
-            float nks = 1.0f, nvs = 1.0f;
-            const bool nvalid = fetch(base + step, nk, nv, nks, nvs);
-
+        // Scores, softmax update and PV product of one step.
+        auto use = [&](Stage& st) __attribute__((always_inline)) {
+            const bool valid = st.valid;
             float kx[P];
-            kr.unpack(kx);
+            st.k.unpack(kx);
             float s[kGH];
             bool need = false;
 #pragma unroll
             for (int g = 0; g < kGH; ++g) {
+                s[g] = kNegInf;
+                if (g >= nh) continue;
                 float x = 0.0f;
 #pragma unroll
                 for (int e = 0; e < P; ++e) x += qv[g][e] * kx[e];
-                s[g] = valid ? sum_parts(x, parts) * ks : kNegInf;
+                s[g] = valid ? sum_parts(x, parts) * st.ks : kNegInf;
                 need |= valid && s[g] > m[g] + kRescaleLog2;
             }
             if (__any(need)) {
 #pragma unroll
                 for (int g = 0; g < kGH; ++g) {
+                    if (g >= nh) break;
                     const float mn = fmaxf(m[g], wave_max(s[g]));
-                    const float alpha = m[g] == kNegInf ? 0.0f : exp2f(m[g] - mn);
+                    const float alpha = m[g] == kNegInf ? 0.0f : __builtin_amdgcn_exp2f(m[g] - mn);
                     l[g] *= alpha;
 #pragma unroll
                     for (int e = 0; e < P; ++e) acc[g][e] *= alpha;
                     m[g] = mn;
                 }
             }
+#pragma unroll
+            for (int i = 0; i < Slice::kW; ++i) st.v.w[i] = valid ? st.v.w[i] : 0u;
+            const float vs = valid ? st.vs : 0.0f;
             float vx[P];
-            vr.unpack(vx);
+            st.v.unpack(vx);
 #pragma unroll
             for (int g = 0; g < kGH; ++g) {
-                const float p = valid ? exp2f(s[g] - m[g]) : 0.0f;
+                if (g >= nh) break;
+                const float p = valid ? __builtin_amdgcn_exp2f(s[g] - m[g]) : 0.0f;
                 l[g] += p;
                 const float pv = p * vs;
 #pragma unroll
                 for (int e = 0; e < P; ++e) acc[g][e] += pv * vx[e];
             }
-            kr = nk;
-            vr = nv;
-            ks = nks;
-            vs = nvs;
-            valid = nvalid;
+        };
+
+        // kStages stages in a ring, loads kStages - 1 steps ahead of use; the loop is
+        // unrolled by kStages so that no stage is copied (a copy would wait for its
+        // loads).
+        if constexpr (GroupedPlan<KVT, P>::kStages == 3) {
+            Stage s0, s1, s2;
+            fetch(t0, s0);
+            fetch(t0 + step, s1);
+            for (int64_t base = t0;; base += 3 * step) {
+                fetch(base + 2 * step, s2);
+                use(s0);
+                if (base + step >= t1) break;
+                fetch(base + 3 * step, s0);
+                use(s1);
+                if (base + 2 * step >= t1) break;
+                fetch(base + 4 * step, s1);
+                use(s2);
+                if (base + 3 * step >= t1) break;
+            }
+        } else {
+            Stage s0, s1;
+            fetch(t0, s0);
+            for (int64_t base = t0;; base += 2 * step) {
+                fetch(base + step, s1);
+                use(s0);
+                if (base + step >= t1) break;
+                fetch(base + 2 * step, s0);
+                use(s1);
+                if (base + 2 * step >= t1) break;
+            }
         }
 
         // Sum the token slots; lanes tok == 0 write their part's dims.
@@ -568,8 +646,10 @@ decode_split_grouped(DecodeArgs a) {
                 for (int g = 0; g < kGH; ++g) {
                     if (g >= nh) break;
                     const float inv = l[g] > 0.0f ? 1.0f / l[g] : 0.0f;
+                    float o[P];
 #pragma unroll
-                    for (int e = 0; e < P; ++e) store_out_any(a, b, hq0 + g, d0 + e, l[g] > 0.0f ? acc[g][e] * inv : 0.0f);
+                    for (int e = 0; e < P; ++e) o[e] = l[g] > 0.0f ? acc[g][e] * inv : 0.0f;
+                    store_out_row<P>(a, b, hq0 + g, d0, o);
                 }
             }
         } else {
