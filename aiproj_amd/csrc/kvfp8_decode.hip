@@ -674,8 +674,12 @@ decode_split_grouped(DecodeArgs a) {
 //   M = max_c m_c; den = sum_c 2^(m_c - M) l_c; num = sum_c 2^(m_c - M) acc_c
 //   out = den > 0 ? num / den : 0
 // One wave per (sequence, q head); sequences with one chunk were written by the
-// split kernel, sequences with none get zeros here.
-template <int QT>
+// split kernel, sequences with none get zeros here. The chunks' (m, l) are read one
+// per lane, 64 chunks at a time, and each lane keeps its chunk's weight; the
+// accumulator rows (lane = dims d, d + 64, ...; ND = ceil(D / 64)) are read four
+// chunks at a time with unconditional loads, so that they are in flight together,
+// each weighted by its chunk's weight read from that chunk's lane.
+template <int QT, int ND>
 __global__ void __launch_bounds__(kDecodeThreads)
 decode_combine(DecodeArgs a) {
     const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
@@ -691,17 +695,62 @@ decode_combine(DecodeArgs a) {
         for (int d = lane; d < D; d += 64) store_out<QT>(a, b, hq, d, 0.0f);
         return;
     }
+    // Consecutive chunks of one (sequence, q head) are num_q_heads states apart.
+    const int64_t p0 = part_index(a, b, 0, hq);
+    const int64_t cs = a.num_q_heads;
     float M = kNegInf;
-    for (int c = 0; c < n; ++c) M = fmaxf(M, a.part_m[part_index(a, b, c, hq)]);
-    for (int d = lane; d < D; d += 64) {
-        float num = 0.0f, den = 0.0f;
-        for (int c = 0; c < n; ++c) {
-            const int64_t pi = part_index(a, b, c, hq);
-            const float wgt = M == kNegInf ? 0.0f : exp2f(a.part_m[pi] - M);
-            den += wgt * a.part_l[pi];
-            num += wgt * a.part_acc[pi * D + d];
+    for (int c0 = 0; c0 < n; c0 += 64) {
+        const int c = c0 + lane;
+        M = fmaxf(M, wave_max(c < n ? a.part_m[p0 + (int64_t)c * cs] : kNegInf));
+    }
+    int dd[ND];
+#pragma unroll
+    for (int i = 0; i < ND; ++i) dd[i] = min(lane + 64 * i, D - 1);
+    float num[ND];
+#pragma unroll
+    for (int i = 0; i < ND; ++i) num[i] = 0.0f;
+    float den = 0.0f;
+    for (int c0 = 0; c0 < n; c0 += 64) {
+        const int c = c0 + lane;
+        float w = 0.0f;
+        if (c < n && M != kNegInf) {
+            const int64_t pi = p0 + (int64_t)c * cs;
+            w = exp2f(a.part_m[pi] - M);
+            den += w * a.part_l[pi];
         }
-        store_out<QT>(a, b, hq, d, den > 0.0f ? num / den : 0.0f);
+        const int cn = min(64, n - c0);
+        int j = 0;
+        for (; j + 4 <= cn; j += 4) {
+            float x[4][ND];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float* row = a.part_acc + (p0 + (int64_t)(c0 + j + u) * cs) * D;
+#pragma unroll
+                for (int i = 0; i < ND; ++i) x[u][i] = row[dd[i]];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float wj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), j + u));
+#pragma unroll
+                for (int i = 0; i < ND; ++i) num[i] += wj * x[u][i];
+            }
+        }
+        for (; j < cn; ++j) {
+            const float* row = a.part_acc + (p0 + (int64_t)(c0 + j) * cs) * D;
+            const float wj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), j));
+#pragma unroll
+            for (int i = 0; i < ND; ++i) num[i] += wj * row[dd[i]];
+        }
+    }
+    den += dpp<kDppXor1>(den);
+    den += dpp<kDppXor2>(den);
+    den += dpp<kDppHalfMirror>(den);
+    den += dpp<kDppMirror>(den);
+    den = sum_rows4(den);
+#pragma unroll
+    for (int i = 0; i < ND; ++i) {
+        const int d = lane + 64 * i;
+        if (d < D) store_out<QT>(a, b, hq, d, den > 0.0f ? num[i] / den : 0.0f);
     }
 }
 
@@ -853,8 +902,11 @@ hipError_t launch_grouped(const DecodeArgs& a, int slice, const Plan& p, hipStre
 template <int QT>
 hipError_t launch_combine(const DecodeArgs& a, hipStream_t s) {
     const int64_t pairs = (int64_t)a.batch * a.num_q_heads;
-    const dim3 grid((unsigned)((pairs + kWavesPerBlock - 1) / kWavesPerBlock));
-    hipLaunchKernelGGL((decode_combine<QT>), grid, dim3(kDecodeThreads), 0, s, a);
+    const dim3 grid((unsigned)((pairs + kWavesPerBlock - 1) / kWavesPerBlock)), block(kDecodeThreads);
+    if (a.head_dim <= 64) hipLaunchKernelGGL((decode_combine<QT, 1>), grid, block, 0, s, a);
+    else if (a.head_dim <= 128) hipLaunchKernelGGL((decode_combine<QT, 2>), grid, block, 0, s, a);
+    else if (a.head_dim <= 256) hipLaunchKernelGGL((decode_combine<QT, 4>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((decode_combine<QT, 8>), grid, block, 0, s, a);
     return hipGetLastError();
 }
 
