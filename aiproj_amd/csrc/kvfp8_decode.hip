@@ -15,9 +15,13 @@
 //      decode_attention.py:437-550) and writes zeros for empty sequences.
 // Scores are kept in the base-2 domain (q * sm_scale * log2 e, then exp2).
 //
-// The split kernel here is the generic VALU one (every cache dtype, any head
-// size up to 512, any group size; one wave per (sequence, chunk, q head)). The
-// FP8 MFMA kernel in kvfp8_decode_mfma.hip is dispatched when its shape
+// The split kernels here run on the vector ALU, for every cache dtype:
+//   * decode_split_grouped: one wave per (sequence, chunk, KV head, group of up to
+//     4 q heads), for 4-byte aligned caches and head sizes D = parts x P with
+//     parts in {4, 8, 16} and P in {4, 8, 16, 20};
+//   * decode_split_generic: one wave per (sequence, chunk, q head), any head size
+//     up to 512 and any alignment.
+// The FP8 MFMA kernel in kvfp8_decode_mfma.hip is dispatched when its shape
 // conditions hold.
 #include "kvfp8_decode_common.h"
 #include "kvfp8_decode_mfma.h"
