@@ -109,11 +109,14 @@ def torch_paged_decode(q: t.Tensor, cache, slots: t.Tensor, lengths: t.Tensor, b
             x = x * scales[rows, offs].unsqueeze(-1)
         return x
 
+    live = (pos[None, :] < lengths[:, None])[:, None, None, :]                   # [B, 1, 1, W]
     k = gather(cache.k, cache.k_scales).permute(0, 2, 3, 1).contiguous()          # [B, Hkv, D, W]
-    v = gather(cache.v, cache.v_scales).permute(0, 2, 1, 3).contiguous()          # [B, Hkv, W, D]
+    # Positions past a sequence's length read whatever its pages (or page 0) hold,
+    # NaN codes included: zero them, as probability 0 times NaN would be NaN.
+    v = gather(cache.v, cache.v_scales).permute(0, 2, 1, 3)                       # [B, Hkv, W, D]
+    v = v.masked_fill(~live.transpose(-1, -2), 0.0).contiguous()
     qg = q.float().view(b, hkv, hq // hkv, d)
     scores = t.matmul(qg, k) / math.sqrt(d)                                       # [B, Hkv, G, W]
-    live = (pos[None, :] < lengths[:, None])[:, None, None, :]
     scores = scores.masked_fill(~live, float("-inf"))
     probs = t.nan_to_num(scores.softmax(dim=-1), nan=0.0)
     return t.matmul(probs, v).reshape(b, hq, d)

@@ -525,3 +525,47 @@ def test_large_batch_with_sixteen_kv_heads():
     expected = oracle_decode(w.q, cache, w.block_table, w.cache_slots, lengths, rows=rows)
     t.testing.assert_close(whole[rows].double().cpu(), t.from_numpy(expected), rtol=NORTH_STAR_RTOL,
                            atol=NORTH_STAR_ATOL)
+
+
+@t.inference_mode()
+@pytest.mark.parametrize("head_dim", [64, 80])
+def test_maximum_batch(head_dim):
+    """8,191 sequences, the most the decode kernels' LDS tile prefix holds (8,192 is
+    refused on the host, tests/test_native_abi.py): D 64 on the MFMA kernel (its
+    prefix and sequence metadata take 64 KB of LDS), D 80 on the grouped VALU kernel.
+    Every row against float32 dequantize-then-attend, sampled rows against the oracle."""
+    from tests.helpers import torch_paged_decode
+
+    batch, hq, hkv = 8191, 8, 2
+    lengths = [(i * 29) % 45 + 1 for i in range(batch)]
+    spec = workloads.WorkloadSpec("max_batch", batch, hq, hkv, head_dim, lengths, seed=18)
+    w = workloads.build(spec, "cuda")
+    cache = PagedKVCache(w.num_blocks, 16, hkv, head_dim, "cuda", FP8)
+    workloads.fill_cache(w, cache, "cuda")
+    k, v = workloads.new_kv(w, "cuda")
+    cache.append_kv(w.new_blocks, w.new_offsets, k, v)
+    ctx = workloads.make_context(w)
+    out = decode_attention_wrapper(w.q, cache, ctx)
+    assert t.isfinite(out).all()
+    ref = torch_paged_decode(w.q, cache, w.cache_slots, ctx.context_lengths, w.block_table)
+    t.testing.assert_close(out.float(), ref, rtol=NORTH_STAR_RTOL, atol=NORTH_STAR_ATOL)
+    rows = [0, 1, 4095, batch - 1]
+    expected = oracle_decode(w.q, cache, w.block_table, w.cache_slots, lengths, rows=rows)
+    t.testing.assert_close(out[rows].double().cpu(), t.from_numpy(expected), rtol=NORTH_STAR_RTOL,
+                           atol=NORTH_STAR_ATOL)
+
+
+@t.inference_mode()
+@pytest.mark.parametrize("cache_dtype", [FP8, t.bfloat16])
+def test_head_dim_512(cache_dtype):
+    # The largest head size the library takes (513 is refused on the host). D 512
+    # splits into none of the grouped kernel's slice widths, so it runs on the
+    # per-q-head VALU kernel; f32 q against the oracle at the reference's tolerance.
+    lengths = [1, 17, 300, 700]
+    hq, hkv, d = 4, 1, 512
+    cache = PagedKVCache(sum(-(-n // 16) for n in lengths) + 4, 16, hkv, d, "cuda", cache_dtype)
+    manager, context, _, _ = fill_decode_batch([cache], lengths, hkv, d, 16, t.bfloat16, seed=19)
+    q = t.randn(len(lengths), hq, d, device="cuda", dtype=t.float32)
+    actual = decode_attention_wrapper(q, cache, context)
+    expected = oracle_decode(q, cache, manager.block_table, context.cache_slots, lengths)
+    t.testing.assert_close(actual.double().cpu(), t.from_numpy(expected), rtol=1e-4, atol=1e-4)

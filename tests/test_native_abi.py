@@ -108,6 +108,16 @@ def test_argument_errors_are_reported_before_any_launch(lib):
                                 4, 16, fake, 4, 64, fake, _native.I64, fake, _native.I32, 0.125,
                                 fake, fake, 16, None)
     assert rc == -5
+    # Sizes beyond the kernels' limits, refused before any launch: batch 8192 (the
+    # decode kernels' LDS tile prefix holds 8191 sequences) and head size 513.
+    rc = lib.kvfp8_paged_decode(fake, _native.BF16, 0, 0, 8192, 8, 2, 64, fake, fake, _native.E4M3FN, fake, fake,
+                                4, 16, fake, 1, 1, fake, _native.I64, fake, _native.I32, 0.125,
+                                fake, fake, 1 << 20, None)
+    assert rc == -6
+    rc = lib.kvfp8_paged_decode(fake, _native.BF16, 0, 0, 1, 8, 2, 513, fake, fake, _native.E4M3FN, fake, fake,
+                                4, 16, fake, 1, 1, fake, _native.I64, fake, _native.I32, 0.125,
+                                fake, fake, 1 << 20, None)
+    assert rc == -6
     # Append: bad index dtype, bad input dtype.
     rc = lib.kvfp8_quantize_append(fake, fake, _native.BF16, 0, 0, 0, 0, fake, _native.F32, fake, _native.I32,
                                    1, 2, 64, 4, 16, fake, fake, fake, fake, None)
