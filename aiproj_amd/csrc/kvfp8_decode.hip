@@ -37,10 +37,8 @@ constexpr int kMaxBatch = 8191;          // LDS prefix of (batch + 1) int32 <= 3
 constexpr int kGenericChunkTokens = 256;
 constexpr int kMaxGrid = 2048;
 
-// Elements of one cache row slice as float32. KvRow<KVT>::load reads `n` elements
-// starting at element e of the cache into x[0 .. n), through 4-byte loads when
-// `dwords` is set (the slice starts on a 4-byte boundary and spans whole dwords),
-// else element by element; x[i] for i >= n is 0.
+// Cache elements as float32, exactly: KvRow<KVT>::unpack converts the kPerDword
+// elements of one dword, KvRow<KVT>::one reads and converts element i.
 template <int KVT> struct KvRow;
 template <> struct KvRow<KVFP8_E4M3FN> {
     static constexpr int kPerDword = 4;
@@ -428,10 +426,6 @@ struct RowSlice {
         const uint32_t* p = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint8_t*>(cache) + e * (4 / kPer));
 #pragma unroll
         for (int i = 0; i < kW; ++i) w[i] = p[i];
-    }
-    __device__ __forceinline__ void clear() {
-#pragma unroll
-        for (int i = 0; i < kW; ++i) w[i] = 0u;
     }
     __device__ __forceinline__ void unpack(float (&x)[P]) const {
 #pragma unroll
