@@ -622,10 +622,21 @@ __device__ __forceinline__ void fetch_new_token(const MfmaArgs& a, int b, int h,
 template <int C>
 __device__ __forceinline__ void put_new_token(const MfmaArgs& a, const NewRow<C>& r, int lane) {
     constexpr int D = 64 * C;
+    // The fetched values enter here: the empty asm (a memory clobber, the values as
+    // operands) keeps the compiler from computing on them earlier, so their wait
+    // comes after the loads the caller issued before this call rather than before
+    // them (which would hold those loads back by one memory round trip).
+    float xk[C], xv[C];
+#pragma unroll
+    for (int e = 0; e < C; ++e) {
+        xk[e] = r.k[e];
+        xv[e] = r.v[e];
+        __asm__ volatile("" : "+v"(xk[e]), "+v"(xv[e]) : : "memory");
+    }
     if (r.row < 0) return;
 #pragma unroll
     for (int kv = 0; kv < 2; ++kv) {
-        const float* x = kv ? r.v : r.k;
+        const float* x = kv ? xv : xk;
         uint32_t amax = abs_bits(x[0]);
 #pragma unroll
         for (int e = 1; e < C; ++e) amax = max(amax, abs_bits(x[e]));
