@@ -447,6 +447,7 @@ def kernel_legs(steps: int):
     enough rotating pools to exceed twice the 256 MB last-level cache:
       * unquantized bf16 caches (the reference's default cache dtype and the control of
         its FP8 tests) at the north-star shape and cfg2, on the same MFMA kernel;
+      * f16 and f32 caches at the north-star shape, on the grouped VALU kernel;
       * MFMA against the generic VALU kernel on the same FP8 bytes (north, cfg4);
       * the generic kernel at head size 80, a shape the MFMA kernel does not take."""
     import torch as t
@@ -457,8 +458,8 @@ def kernel_legs(steps: int):
     legs = {}
 
     def pools_for(w, dtype, spec):
-        per_token = spec.num_kv_heads * (2 * spec.head_dim * (1 if dtype == t.float8_e4m3fn else 2)
-                                         + (8 if dtype == t.float8_e4m3fn else 0))
+        esize = t.empty((), dtype=dtype).element_size()
+        per_token = spec.num_kv_heads * (2 * spec.head_dim * esize + (8 if dtype == t.float8_e4m3fn else 0))
         pool = w.num_blocks * spec.block_size * per_token
         count = max(2, math.ceil(2 * MALL_BYTES / pool) + 1)
         caches = []
@@ -485,6 +486,17 @@ def kernel_legs(steps: int):
             split_us, call_us = _time_decode(caches, w.q, workloads.make_context(w), steps)
             legs[f"bf16_cache_{name}"] = entry(spec, 2, split_us, call_us, "decode_mfma_kernel (bf16 cache)")
             log(f"[bf16 cache {name}] split {split_us:.1f} us, split + combine {call_us:.1f} us")
+            del caches
+            t.cuda.empty_cache()
+        # The other unquantized cache dtypes the reference accepts take the grouped VALU kernel.
+        spec = workloads.spec("north")
+        w = workloads.build(spec, "cuda")
+        for dtype, esize, tag in ((t.float16, 2, "f16"), (t.float32, 4, "f32")):
+            caches = pools_for(w, dtype, spec)
+            split_us, call_us = _time_decode(caches, w.q, workloads.make_context(w), max(4, steps // 2))
+            legs[f"{tag}_cache_north"] = entry(spec, esize, split_us, call_us,
+                                               f"decode_split_grouped + decode_combine ({tag} cache)")
+            log(f"[{tag} cache north] split {split_us:.1f} us, split + combine {call_us:.1f} us")
             del caches
             t.cuda.empty_cache()
         for name in ("north", "cfg4"):
