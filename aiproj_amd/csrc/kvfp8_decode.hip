@@ -927,16 +927,20 @@ KernelTiming kvfp8::next_kernel_timing() {
 namespace {
 
 // Whether a call runs on the MFMA kernel: the plan allows it, the caches are
-// 16-byte aligned, and slot * 32 + count fits the kernel's int32 per sequence.
-bool takes_mfma(const Plan& p, const void* k_cache, const void* v_cache, int64_t bt_rows) {
+// 16-byte aligned, an f16 cache comes with f16 q, and slot * 32 + count fits the
+// kernel's int32 per sequence.
+bool takes_mfma(const Plan& p, const void* k_cache, const void* v_cache, int64_t bt_rows, int q_dtype,
+                int kv_dtype) {
     const bool aligned = (((uintptr_t)k_cache | (uintptr_t)v_cache) & 15) == 0;
-    return p.mfma && aligned && bt_rows < ((int64_t)1 << 26);
+    // An f16 cache runs on f16 products, which take f16 q exactly and nothing else.
+    const bool operands = kv_dtype != KVFP8_F16 || q_dtype == KVFP8_F16;
+    return p.mfma && aligned && operands && bt_rows < ((int64_t)1 << 26);
 }
 
 template <int QT>
 hipError_t dispatch_kv(const DecodeArgs& a, int kv_dtype, const Plan& p, void* workspace, hipStream_t s,
                        int phases) {
-    if (takes_mfma(p, a.k_cache, a.v_cache, a.bt_rows))
+    if (takes_mfma(p, a.k_cache, a.v_cache, a.bt_rows, a.q_dtype, kv_dtype))
         return launch_mfma_decode<QT>(a, kv_dtype, workspace, s, phases);
     if (phases & kPhaseSplit) {
         const int64_t units_total = (int64_t)a.batch * p.max_chunks * a.num_q_heads;
@@ -1075,7 +1079,7 @@ int paged_decode(const void* q, int q_dtype, int64_t q_stride_b, int64_t q_strid
     if (kv_dtype == KVFP8_E4M3FN && (!k_scales || !v_scales)) return KVFP8_ENULL;
 
     const Plan p = make_plan(batch, num_q_heads, num_kv_heads, head_dim, bt_width, block_size, kv_dtype);
-    const bool mfma = takes_mfma(p, k_cache, v_cache, bt_rows);
+    const bool mfma = takes_mfma(p, k_cache, v_cache, bt_rows, q_dtype, kv_dtype);
     const int64_t need = workspace_taken(p, mfma, batch, num_q_heads, num_kv_heads, head_dim);
     if (use_scratch) {
         if (need > kScratchBytes) return KVFP8_ELIMIT;

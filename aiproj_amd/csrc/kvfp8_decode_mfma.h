@@ -5,8 +5,9 @@
 
 namespace kvfp8 {
 
-// Shapes the MFMA kernel handles (e4m3fn or bf16 cache, D in {64, 128}, page size
-// a multiple of 16, group size <= 16); everything else goes to the generic kernel.
+// Shapes the MFMA kernel handles (e4m3fn, bf16 or f16 cache, D in {64, 128}, page
+// size a multiple of 16, group size <= 16; an f16 cache also needs f16 q, which the
+// caller checks); everything else goes to the VALU kernels.
 bool mfma_decode_supported(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                            int64_t bt_width, int32_t block_size, int kv_dtype);
 

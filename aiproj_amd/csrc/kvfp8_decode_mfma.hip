@@ -47,6 +47,8 @@
 //     of one column and v_cvt_scalef32_pk_bf16_fp8 widens the pair.
 #include "kvfp8_decode_mfma.h"
 
+#include <type_traits>
+
 namespace kvfp8 {
 
 namespace {
@@ -54,6 +56,7 @@ namespace {
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
@@ -108,6 +111,14 @@ __device__ __forceinline__ bf16x8_t fp8x8(uint32_t x0, uint32_t x1) {
 __device__ __forceinline__ f32x4_t mma(bf16x8_t a, bf16x8_t b, f32x4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
+__device__ __forceinline__ f32x4_t mma(f16x8_t a, f16x8_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// Operand type of the products: bf16 (e4m3fn codes widen to it exactly, bf16 caches
+// are it), or f16 for an f16 cache read with f16 q (both exact in f16).
+template <bool kF16> using OpT = std::conditional_t<kF16, f16x8_t, bf16x8_t>;
+template <bool kF16> using OpE = std::conditional_t<kF16, _Float16, __bf16>;
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -341,10 +352,11 @@ __device__ __forceinline__ void load_q_raw(const MfmaArgs& a, int b, int h, int 
     }
 }
 
-// Q^T operands from the raw elements: bf16 (f32 and f16 q as hi + lo parts),
-// zero for heads g >= G and for operands not loaded.
-template <int C, int ES, int QT, int kOps, bool kHiLo>
-__device__ __forceinline__ void q_operands(const QRaw<C, QT>& r, int G, int lane, bf16x8_t* qh, bf16x8_t* ql) {
+// Q^T operands from the raw elements: bf16 (f32 and f16 q as hi + lo parts) or f16
+// (f16 q, exact), zero for heads g >= G and for operands not loaded.
+template <int C, int ES, int QT, int kOps, bool kHiLo, bool kF16>
+__device__ __forceinline__ void q_operands(const QRaw<C, QT>& r, int G, int lane, OpT<kF16>* qh, OpT<kF16>* ql) {
+    using E = OpE<kF16>;
     using T = typename Elem<QT>::T;
     const int c = lane & 15;
 #pragma unroll
@@ -358,17 +370,20 @@ __device__ __forceinline__ void q_operands(const QRaw<C, QT>& r, int G, int lane
                 else x = Elem<QT>::load((T)((r.w[kb][i >> 1] >> (16 * (i & 1))) & 0xFFFFu));
             }
             x = live ? x : 0.0f;
-            const __bf16 hi = (__bf16)x;
+            const E hi = (E)x;
             qh[kb][i] = hi;
-            if constexpr (kHiLo) ql[kb][i] = (__bf16)(x - (float)hi);
+            if constexpr (kHiLo) ql[kb][i] = (E)(x - (float)hi);
         }
     }
 }
 
-template <int C, int ES, bool kHiLo, int kSets>
-__device__ __forceinline__ void compute_step(WaveState<C>& st, const StepData<C, ES>& s, const bf16x8_t* qh,
-                                             const bf16x8_t* ql, float4* stage, int lane, int lim_a,
+template <int C, int ES, bool kHiLo, int kSets, bool kF16>
+__device__ __forceinline__ void compute_step(WaveState<C>& st, const StepData<C, ES>& s, const OpT<kF16>* qh,
+                                             const OpT<kF16>* ql, float4* stage, int lane, int lim_a,
                                              int lim_b, float score_scale) {
+    static_assert(!kF16 || ES == 2, "f16 operands come from an f16 cache");
+    using Op = OpT<kF16>;
+    using E = OpE<kF16>;
     constexpr int VW = C * ES;
     const int j = lane >> 4;
     const bool full = lim_a == 16 && lim_b == 16;   // wave-uniform
@@ -458,14 +473,14 @@ __device__ __forceinline__ void compute_step(WaveState<C>& st, const StepData<C,
         f32x4_t sa = {0.0f, 0.0f, 0.0f, 0.0f}, sb = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int kb = 0; kb < 2 * C; ++kb) {
-            bf16x8_t ka, kbv;
+            Op ka, kbv;
             if constexpr (ES == 1) {
                 const int c = kb >> 1, half = kb & 1;
                 ka = fp8x8(s.ka[c][2 * half], s.ka[c][2 * half + 1]);
                 kbv = fp8x8(s.kb[c][2 * half], s.kb[c][2 * half + 1]);
             } else {
-                ka = __builtin_bit_cast(bf16x8_t, s.ka[kb]);
-                kbv = __builtin_bit_cast(bf16x8_t, s.kb[kb]);
+                ka = __builtin_bit_cast(Op, s.ka[kb]);
+                kbv = __builtin_bit_cast(Op, s.kb[kb]);
             }
             sa = mma(ka, qh[kb], sa);
             sb = mma(kbv, qh[kb], sb);
@@ -516,11 +531,11 @@ __device__ __forceinline__ void compute_step(WaveState<C>& st, const StepData<C,
         for (int i = 0; i < 8; ++i)
             if (!live[i]) pv[i] = 0.0f;
     }
-    bf16x8_t ph, pl;
+    Op ph, pl;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        ph[i] = (__bf16)pv[i];
-        if constexpr (kHiLo) pl[i] = (__bf16)(pv[i] - (float)ph[i]);
+        ph[i] = (E)pv[i];
+        if constexpr (kHiLo) pl[i] = (E)(pv[i] - (float)ph[i]);
     }
 
     // V rows: zero the rows of masked tokens (stale pages may hold NaN).
@@ -559,7 +574,7 @@ __device__ __forceinline__ void compute_step(WaveState<C>& st, const StepData<C,
             u32x4_t w;
 #pragma unroll
             for (int p = 0; p < 4; ++p) w[p] = __builtin_amdgcn_perm(vr[2 * p + 1][nb >> 1], vr[2 * p][nb >> 1], sel);
-            const bf16x8_t av = __builtin_bit_cast(bf16x8_t, w);
+            const Op av = __builtin_bit_cast(Op, w);
             st.o[nb] = mma(av, ph, st.o[nb]);
             if constexpr (kHiLo) st.o[nb] = mma(av, pl, st.o[nb]);
         }
@@ -659,12 +674,14 @@ __device__ __forceinline__ void put_new_token(const MfmaArgs& a, const NewRow<C>
     }
 }
 
-template <int C, int QT, int ES, int kSets, bool kAppend>
+template <int C, int QT, int ES, int kSets, bool kAppend, bool kF16>
 __global__ void __launch_bounds__(kMaxThreads)
 decode_mfma_kernel(MfmaArgs a) {
     constexpr int D = 64 * C;
     constexpr int NB = 4 * C;
-    constexpr bool kHiLo = QT != KVFP8_BF16;
+    // q as bf16 hi + lo unless it is the operand type already (bf16 q on bf16
+    // operands, f16 q on f16 operands).
+    constexpr bool kHiLo = kF16 ? QT != KVFP8_F16 : QT != KVFP8_BF16;
     extern __shared__ int32_t prefix[];                // [batch + 1], then meta [batch]
     __shared__ int32_t wave_total[kMaxWaves];
     __shared__ float4 stage_all[kMaxWaves][16];
@@ -787,15 +804,15 @@ decode_mfma_kernel(MfmaArgs a) {
             if constexpr (kAppend) {
                 if (append && !put_early) put_new_token<C>(a, fresh, lane);
             }
-            bf16x8_t qh[2 * C], ql[2 * C];
-            q_operands<C, ES, QT, kQOps, kHiLo>(qraw, G, lane, qh, ql);
+            OpT<kF16> qh[2 * C], ql[2 * C];
+            q_operands<C, ES, QT, kQOps, kHiLo, kF16>(qraw, G, lane, qh, ql);
 
 
             auto compute = [&](const StepData<C, ES>& cur, int32_t tile0, const TileRef& ra, const TileRef& rb) {
                 const int64_t pos = (int64_t)tile0 * 16;
                 const int lim_a = ra.valid ? (int)max((int64_t)0, min((int64_t)16, len - pos)) : 0;
                 const int lim_b = rb.valid ? (int)max((int64_t)0, min((int64_t)16, len - pos - 16)) : 0;
-                compute_step<C, ES, kHiLo, kSets>(st, cur, qh, ql, stage, lane, lim_a, lim_b, a.d.score_scale);
+                compute_step<C, ES, kHiLo, kSets, kF16>(st, cur, qh, ql, stage, lane, lim_a, lim_b, a.d.score_scale);
             };
             if constexpr (ES == 1) {
                 while (true) {
@@ -986,7 +1003,7 @@ int64_t max_groups(int32_t num_kv_heads) {
     return (int64_t)device_cus() * (per_cu > 0 ? per_cu : 1);
 }
 
-template <int C, int QT, int ES, int kSets, bool kAppend = false>
+template <int C, int QT, int ES, int kSets, bool kAppend = false, bool kF16 = false>
 hipError_t launch_c(const MfmaArgs& a, int64_t cap, hipStream_t s, int phases) {
     const int threads = 64 * waves_for(a.d.num_kv_heads);
     const size_t lds = (size_t)(2 * a.d.batch + 1) * sizeof(int32_t);
@@ -1000,7 +1017,7 @@ hipError_t launch_c(const MfmaArgs& a, int64_t cap, hipStream_t s, int phases) {
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
     int& per_cu = resident[dev][threads / 64];
     if (per_cu == 0) {
-        const void* fn = reinterpret_cast<const void*>(&decode_mfma_kernel<C, QT, ES, kSets, kAppend>);
+        const void* fn = reinterpret_cast<const void*>(&decode_mfma_kernel<C, QT, ES, kSets, kAppend, kF16>);
         int n = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, threads, 0) != hipSuccess || n <= 0) n = 1;
         per_cu = n;
@@ -1016,7 +1033,7 @@ hipError_t launch_c(const MfmaArgs& a, int64_t cap, hipStream_t s, int phases) {
     int64_t groups = (int64_t)device_cus() * (fit > 0 ? fit : 1);
     groups = groups < cap ? groups : cap;
     if (phases & kPhaseSplit) {
-        const hipError_t err = launch_timed(decode_mfma_kernel<C, QT, ES, kSets, kAppend>, dim3((unsigned)groups), dim3(threads),
+        const hipError_t err = launch_timed(decode_mfma_kernel<C, QT, ES, kSets, kAppend, kF16>, dim3((unsigned)groups), dim3(threads),
                                             lds, s, next_kernel_timing(), a);
         if (err != hipSuccess) return err;
     }
@@ -1030,7 +1047,7 @@ hipError_t launch_c(const MfmaArgs& a, int64_t cap, hipStream_t s, int phases) {
 
 bool mfma_decode_supported(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                            int64_t bt_width, int32_t block_size, int kv_dtype) {
-    if (kv_dtype != KVFP8_E4M3FN && kv_dtype != KVFP8_BF16) return false;
+    if (kv_dtype != KVFP8_E4M3FN && kv_dtype != KVFP8_BF16 && kv_dtype != KVFP8_F16) return false;
     if (head_dim != 64 && head_dim != 128) return false;
     if (block_size < 16 || block_size % 16 != 0) return false;
     if (num_q_heads % num_kv_heads != 0 || num_q_heads / num_kv_heads > 16) return false;
@@ -1080,6 +1097,13 @@ hipError_t launch_mfma_decode(const DecodeArgs& d, int kv_dtype, void* workspace
     if (kv_dtype == KVFP8_BF16)
         return d.head_dim == 64 ? launch_c<1, QT, 2, 1>(a, cap, stream, phases)
                                 : launch_c<2, QT, 2, 1>(a, cap, stream, phases);
+    if (kv_dtype == KVFP8_F16) {
+        // f16 cache with f16 q (the caller checked): f16 operands.
+        if constexpr (QT == KVFP8_F16)
+            return d.head_dim == 64 ? launch_c<1, QT, 2, 1, false, true>(a, cap, stream, phases)
+                                    : launch_c<2, QT, 2, 1, false, true>(a, cap, stream, phases);
+        else return hipErrorInvalidValue;
+    }
     if (d.new_k != nullptr) {
         // Fused append + decode (e4m3fn only; the caller checked the shape).
         if (d.head_dim == 64) return launch_c<1, QT, 1, 1, true>(a, cap, stream, phases);

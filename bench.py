@@ -447,7 +447,8 @@ def kernel_legs(steps: int):
     enough rotating pools to exceed twice the 256 MB last-level cache:
       * unquantized bf16 caches (the reference's default cache dtype and the control of
         its FP8 tests) at the north-star shape and cfg2, on the same MFMA kernel;
-      * f16 and f32 caches at the north-star shape, on the grouped VALU kernel;
+      * f16 (with f16 q, on the MFMA kernel) and f32 (grouped VALU kernel) caches at the
+        north-star shape;
       * MFMA against the generic VALU kernel on the same FP8 bytes (north, cfg4);
       * the generic kernel at head size 80, a shape the MFMA kernel does not take."""
     import torch as t
@@ -471,9 +472,10 @@ def kernel_legs(steps: int):
             caches.append(cache)
         return caches
 
-    def entry(spec, kv_bytes, split_us, call_us, kernel):
+    def entry(spec, kv_bytes, split_us, call_us, kernel, q_bytes=2):
         nbytes = oracle.decode_algorithmic_bytes(spec.lengths, spec.num_q_heads, spec.num_kv_heads, spec.head_dim,
-                                                 spec.block_size, kv_bytes=kv_bytes)
+                                                 spec.block_size, q_bytes=q_bytes, out_bytes=q_bytes,
+                                                 kv_bytes=kv_bytes)
         return {"kernel": kernel, "kv_tokens": spec.total_tokens, "algorithmic_bytes": nbytes,
                 "split_us": round(split_us, 2), "split_frac": round(nbytes / (split_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
                 "call_us": round(call_us, 2), "call_frac": round(nbytes / (call_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)}
@@ -488,14 +490,16 @@ def kernel_legs(steps: int):
             log(f"[bf16 cache {name}] split {split_us:.1f} us, split + combine {call_us:.1f} us")
             del caches
             t.cuda.empty_cache()
-        # The other unquantized cache dtypes the reference accepts take the grouped VALU kernel.
+        # The other unquantized cache dtypes the reference accepts: f16 read with f16 q
+        # (an f16 model) on the MFMA kernel's f16 products, f32 on the grouped VALU kernel.
         spec = workloads.spec("north")
         w = workloads.build(spec, "cuda")
-        for dtype, esize, tag in ((t.float16, 2, "f16"), (t.float32, 4, "f32")):
+        for dtype, esize, tag, kernel in ((t.float16, 2, "f16", "decode_mfma_kernel (f16 cache, f16 q)"),
+                                          (t.float32, 4, "f32", "decode_split_grouped + decode_combine (f32 cache)")):
             caches = pools_for(w, dtype, spec)
-            split_us, call_us = _time_decode(caches, w.q, workloads.make_context(w), max(4, steps // 2))
-            legs[f"{tag}_cache_north"] = entry(spec, esize, split_us, call_us,
-                                               f"decode_split_grouped + decode_combine ({tag} cache)")
+            q = w.q.to(dtype)
+            split_us, call_us = _time_decode(caches, q, workloads.make_context(w), max(4, steps // 2))
+            legs[f"{tag}_cache_north"] = entry(spec, esize, split_us, call_us, kernel, q_bytes=esize)
             log(f"[{tag} cache north] split {split_us:.1f} us, split + combine {call_us:.1f} us")
             del caches
             t.cuda.empty_cache()

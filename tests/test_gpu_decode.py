@@ -569,3 +569,25 @@ def test_head_dim_512(cache_dtype):
     actual = decode_attention_wrapper(q, cache, context)
     expected = oracle_decode(q, cache, manager.block_table, context.cache_slots, lengths)
     t.testing.assert_close(actual.double().cpu(), t.from_numpy(expected), rtol=1e-4, atol=1e-4)
+
+
+@t.inference_mode()
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("num_q_heads,num_kv_heads", [(8, 2), (32, 8), (16, 1), (4, 4)])
+def test_f16_cache_decode(head_dim, num_q_heads, num_kv_heads):
+    # An f16 cache read with f16 q runs on f16 matrix products (both operands exact in
+    # f16); with bf16 or f32 q it runs on the VALU kernel. Each against the oracle at
+    # the reference's tolerance for its q dtype.
+    block_size = 16
+    num_blocks = sum(-(-n // 16) for n in DECODE_LENGTHS) + 4
+    cache = PagedKVCache(num_blocks, block_size, num_kv_heads, head_dim, "cuda", t.float16)
+    manager, context, _, _ = fill_decode_batch([cache], DECODE_LENGTHS, num_kv_heads, head_dim, block_size,
+                                               t.float16, seed=20)
+    base = t.randn(len(DECODE_LENGTHS), num_q_heads, head_dim, device="cuda")
+    for q_dtype in (t.float16, t.bfloat16, t.float32):
+        q = base.to(q_dtype)
+        actual = decode_attention_wrapper(q, cache, context)
+        assert actual.dtype == q_dtype
+        expected = oracle_decode(q, cache, manager.block_table, context.cache_slots, DECODE_LENGTHS)
+        tol = OUTPUT_TOLERANCE[q_dtype]
+        t.testing.assert_close(actual.double().cpu(), t.from_numpy(expected), rtol=tol, atol=tol)
