@@ -207,14 +207,17 @@ def test_decode_edge_cases_and_calling_forms():
 
 
 @t.inference_mode()
-def test_decode_block_sizes_other_than_16():
-    # Page sizes under 16 take the VALU kernel; 1 and 2 fill its whole per-wave
-    # page list (256 entries for a 256-token chunk).
-    for block_size in (1, 2, 4, 8, 32, 64):
-        lengths = [3, 40, 129]
-        cache = PagedKVCache(sum(-(-n // block_size) for n in lengths) + 4, block_size, 2, 64, "cuda", FP8)
-        manager, context, _, _ = fill_decode_batch([cache], lengths, 2, 64, block_size, t.bfloat16, seed=10)
-        q = t.randn(3, 8, 64, device="cuda", dtype=t.float32)
+@pytest.mark.parametrize("head_dim", [64, 80])
+def test_decode_block_sizes_other_than_16(head_dim):
+    # D 64: page sizes under 16 take the VALU kernel, 32 and up the MFMA kernel; D 80
+    # always the grouped VALU kernel. Pages of 1 and 2 fill its whole per-wave page
+    # list (256 entries for a 256-token chunk); pages of 256 and 512 hold a whole chunk
+    # (one entry), and lengths past 600 cross pages and chunks.
+    for block_size in (1, 2, 4, 8, 32, 64, 256, 512):
+        lengths = [3, 40, 129, 700]
+        cache = PagedKVCache(sum(-(-n // block_size) for n in lengths) + 4, block_size, 2, head_dim, "cuda", FP8)
+        manager, context, _, _ = fill_decode_batch([cache], lengths, 2, head_dim, block_size, t.bfloat16, seed=10)
+        q = t.randn(len(lengths), 8, head_dim, device="cuda", dtype=t.float32)
         out = decode_attention_wrapper(q, cache, context)
         expected = oracle_decode(q, cache, manager.block_table, context.cache_slots, lengths)
         t.testing.assert_close(out.double().cpu(), t.from_numpy(expected), rtol=1e-4, atol=1e-4)
