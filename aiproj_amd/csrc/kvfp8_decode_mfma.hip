@@ -929,10 +929,14 @@ combine_mfma_kernel(MfmaArgs a) {
     if (w0 == w1) return;    // finished by the decode kernel
     const int32_t pieces = w1 - w0 + 1;
     const int64_t hq_count = a.d.num_q_heads;
+    // Piece i is in workgroup w0 + i. The workgroups after w0 start inside the
+    // sequence, so it is their first segment (state 2 w); w0 holds it as its first
+    // segment only when its range starts at t0, else as its last (state 2 w + 1).
+    // One division per wave instead of one per piece.
+    const int32_t cut0 = (int64_t)w0 * total / groups < t0 ? 1 : 0;
     auto state_index = [&](int32_t i) -> int64_t {
         const int64_t w = w0 + i;
-        const int64_t start = w * total / groups;
-        return (2 * w + (start >= t0 ? 0 : 1)) * hq_count + hq;
+        return (2 * w + (i == 0 ? cut0 : 0)) * hq_count + hq;
     };
 
     // Each lane merges its pieces online (all loads independent, issued
