@@ -594,18 +594,28 @@ __device__ __forceinline__ void compute_step(WaveState<C>& st, const StepData<C,
 // quantizes and stores; the wave's own loads of that page row come after put()
 // in its instruction order, which the memory pipeline keeps for one wave, so
 // they read the new codes and scales.
+// fetch() issues every load at once, with no branch and no wait in front of them:
+// the kernel-argument fields are read together, the write location as two dword
+// scalar loads per index (the low word, then the high word of an int64 entry or
+// the low word again of an int32 one), and each element as two 16-bit loads (the
+// two halves of a float32, or the 16-bit value twice), all at element alignment.
+// The range check and the conversion to float wait for put(), which runs after
+// the wave has issued its first K/V loads.
 template <int C>
 struct NewRow {
-    float k[C], v[C];
-    int64_t row;      // cache row (page slot * Hkv + h), or -1: no write
+    uint32_t k_lo[C], k_hi[C], v_lo[C], v_hi[C];   // the two 16-bit loads of each element
+    uint32_t page_lo, page_hi, off_lo, off_hi;
+    int32_t idx64;         // bit 0: new_blocks is int64; bit 1: new_offsets is int64
+    int32_t dtype;
+    int32_t h;             // KV head
 };
 
-typedef const __attribute__((address_space(4))) int64_t* const_i64_ptr;
+typedef const __attribute__((address_space(4))) uint32_t* const_u32_ptr;
+typedef const __attribute__((address_space(1))) uint16_t* const_g_u16_ptr;   // global memory
 
 template <int C>
 __device__ __forceinline__ void fetch_new_token(const MfmaArgs& a, int b, int h, int lane, NewRow<C>& r) {
     constexpr int D = 64 * C;
-    r.row = -1;
     // The new-row fields are read from the kernel-argument segment here, where they
     // are used: the empty asm keeps the compiler from hoisting these loads to the
     // kernel's entry and holding them in scalar registers through the step loop.
@@ -613,24 +623,34 @@ __device__ __forceinline__ void fetch_new_token(const MfmaArgs& a, int b, int h,
     __asm__ volatile("" : "+s"(kargs));
     typedef const __attribute__((address_space(4))) DecodeArgs* const_args_ptr;
     const_args_ptr na = (const_args_ptr)(uintptr_t)(kargs + offsetof(MfmaArgs, d));
+    const uint64_t pb = (uint64_t)(uintptr_t)na->new_blocks, po = (uint64_t)(uintptr_t)na->new_offsets;
+    const int32_t b64 = na->new_blocks64, o64 = na->new_offsets64;
+    const int32_t dtype = na->new_dtype;
+    const int64_t k_sb = na->new_k_sb, v_sb = na->new_v_sb;
+    const uint64_t src_k = (uint64_t)(uintptr_t)na->new_k, src_v = (uint64_t)(uintptr_t)na->new_v;
     // Write location: scalar loads (their wait does not cover the vector loads in
     // flight). The index arrays are read-only for the whole kernel.
-    const uint64_t pb = (uint64_t)(uintptr_t)na->new_blocks, po = (uint64_t)(uintptr_t)na->new_offsets;
-    const int64_t page = na->new_blocks64 ? ((const_i64_ptr)pb)[b] : (int64_t)((const_i32_ptr)pb)[b];
-    const int64_t off = na->new_offsets64 ? ((const_i64_ptr)po)[b] : (int64_t)((const_i32_ptr)po)[b];
-    if (page < 0 || page >= a.d.num_blocks || off < 0 || off >= a.d.block_size) return;
-    r.row = (page * a.d.block_size + off) * a.d.num_kv_heads + h;
-    const int dtype = na->new_dtype;
+    const uint64_t pb_at = pb + (uint64_t)b * (b64 ? 8 : 4), po_at = po + (uint64_t)b * (o64 ? 8 : 4);
+    r.page_lo = *(const_u32_ptr)pb_at;
+    r.page_hi = *(const_u32_ptr)(pb_at + (b64 ? 4 : 0));
+    r.off_lo = *(const_u32_ptr)po_at;
+    r.off_hi = *(const_u32_ptr)(po_at + (o64 ? 4 : 0));
+    r.idx64 = (b64 ? 1 : 0) | (o64 ? 2 : 0);
+    r.dtype = dtype;
+    r.h = h;
+    const uint64_t esz = dtype == KVFP8_F32 ? 4 : 2;
+    const uint64_t hi_step = dtype == KVFP8_F32 ? 2 : 0;
 #pragma unroll
     for (int kv = 0; kv < 2; ++kv) {
-        const int64_t src_off = (int64_t)b * (kv ? na->new_v_sb : na->new_k_sb) + (int64_t)h * D + C * lane;
-        const void* src = kv ? na->new_v : na->new_k;
-        float* x = kv ? r.v : r.k;
+        const uint64_t row = (kv ? src_v : src_k) + ((uint64_t)b * (uint64_t)(kv ? v_sb : k_sb) + (uint64_t)h * D) * esz;
+        uint32_t* lo = kv ? r.v_lo : r.k_lo;
+        uint32_t* hi = kv ? r.v_hi : r.k_hi;
 #pragma unroll
-        for (int e = 0; e < C; ++e)
-            x[e] = dtype == KVFP8_F32 ? reinterpret_cast<const float*>(src)[src_off + e]
-                 : dtype == KVFP8_F16 ? f16_to_f32(reinterpret_cast<const uint16_t*>(src)[src_off + e])
-                                      : bf16_to_f32(reinterpret_cast<const uint16_t*>(src)[src_off + e]);
+        for (int e = 0; e < C; ++e) {
+            const uint64_t at = row + (uint64_t)(C * lane + e) * esz;
+            lo[e] = *(const_g_u16_ptr)(uintptr_t)at;
+            hi[e] = *(const_g_u16_ptr)(uintptr_t)(at + hi_step);
+        }
     }
 }
 
@@ -641,14 +661,26 @@ __device__ __forceinline__ void put_new_token(const MfmaArgs& a, const NewRow<C>
     // operands) keeps the compiler from computing on them earlier, so their wait
     // comes after the loads the caller issued before this call rather than before
     // them (which would hold those loads back by one memory round trip).
+    uint32_t rk[C], rv[C];
+#pragma unroll
+    for (int e = 0; e < C; ++e) {
+        uint32_t kl = r.k_lo[e], kh = r.k_hi[e], vl = r.v_lo[e], vh = r.v_hi[e];
+        __asm__ volatile("" : "+v"(kl), "+v"(kh), "+v"(vl), "+v"(vh) : : "memory");
+        rk[e] = kl | (kh << 16);     // float32 bits, or the 16-bit value in the low half
+        rv[e] = vl | (vh << 16);
+    }
+    const int64_t page = (r.idx64 & 1) ? (int64_t)(((uint64_t)r.page_hi << 32) | r.page_lo) : (int64_t)(int32_t)r.page_lo;
+    const int64_t off = (r.idx64 & 2) ? (int64_t)(((uint64_t)r.off_hi << 32) | r.off_lo) : (int64_t)(int32_t)r.off_lo;
+    if (page < 0 || page >= a.d.num_blocks || off < 0 || off >= a.d.block_size) return;
+    const int64_t row = (page * a.d.block_size + off) * a.d.num_kv_heads + r.h;
     float xk[C], xv[C];
 #pragma unroll
     for (int e = 0; e < C; ++e) {
-        xk[e] = r.k[e];
-        xv[e] = r.v[e];
-        __asm__ volatile("" : "+v"(xk[e]), "+v"(xv[e]) : : "memory");
+        xk[e] = r.dtype == KVFP8_F32 ? __uint_as_float(rk[e])
+              : r.dtype == KVFP8_F16 ? f16_to_f32((uint16_t)rk[e]) : bf16_to_f32((uint16_t)rk[e]);
+        xv[e] = r.dtype == KVFP8_F32 ? __uint_as_float(rv[e])
+              : r.dtype == KVFP8_F16 ? f16_to_f32((uint16_t)rv[e]) : bf16_to_f32((uint16_t)rv[e]);
     }
-    if (r.row < 0) return;
 #pragma unroll
     for (int kv = 0; kv < 2; ++kv) {
         const float* x = kv ? xv : xk;
@@ -667,10 +699,10 @@ __device__ __forceinline__ void put_new_token(const MfmaArgs& a, const NewRow<C>
             codes = clamp_encode(x[0] / scale);
             if constexpr (C > 1) codes |= (uint32_t)clamp_encode(x[C - 1] / scale) << 8;
         }
-        uint8_t* dst = reinterpret_cast<uint8_t*>(const_cast<void*>(kv ? a.d.v_cache : a.d.k_cache)) + r.row * D + C * lane;
+        uint8_t* dst = reinterpret_cast<uint8_t*>(const_cast<void*>(kv ? a.d.v_cache : a.d.k_cache)) + row * D + C * lane;
         if constexpr (C == 2) *reinterpret_cast<uint16_t*>(dst) = (uint16_t)codes;
         else *dst = (uint8_t)codes;
-        if (lane == 0) const_cast<float*>(kv ? a.d.v_scales : a.d.k_scales)[r.row] = scale;
+        if (lane == 0) const_cast<float*>(kv ? a.d.v_scales : a.d.k_scales)[row] = scale;
     }
 }
 
