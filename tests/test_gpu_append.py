@@ -182,6 +182,44 @@ def test_golden_quantize_cases_on_gpu():
 
 
 @t.inference_mode()
+@pytest.mark.parametrize("input_dtype,head_dim,hkv,index_dtype,tokens", [
+    (t.bfloat16, 128, 4, t.int32, 65536 + 37),       # the cfg5 prefill layer plus a ragged tail
+    (t.float16, 80, 2, t.int64, 131072 + 11),        # lanes past D in every row
+    (t.float32, 64, 8, t.int32, 65536 + 5),          # four lanes per row
+])
+def test_fp8_append_at_prefill_sizes(input_dtype, head_dim, hkv, index_dtype, tokens):
+    # Row counts above the multi-row kernel's threshold (4096 blocks of 4 passes):
+    # shuffled slots, a few write locations outside the pool, bit-exact against the
+    # oracle, untouched slots unchanged.
+    g = t.Generator(device="cuda").manual_seed(tokens)
+    num_blocks = tokens // 16 + 8
+    slots = t.randperm(num_blocks * 16, device="cuda", generator=g)[:tokens]
+    blocks, offsets = (slots // 16).to(index_dtype), (slots % 16).to(index_dtype)
+    outside = t.tensor([0, 7, tokens // 2, tokens - 1], device="cuda")
+    blocks[outside[:2]] = t.tensor([-1, num_blocks], dtype=index_dtype, device="cuda")
+    offsets[outside[2:]] = t.tensor([16, -3], dtype=index_dtype, device="cuda")
+    cache = PagedKVCache(num_blocks, 16, hkv, head_dim, "cuda", FP8)
+    cache.k.view(t.uint8).fill_(0x5A)
+    cache.k_scales.fill_(-1.0)
+    ks = t.randn(tokens, hkv, head_dim, device="cuda", generator=g).to(input_dtype)
+    vs = (t.randn(tokens, hkv, head_dim, device="cuda", generator=g) * 1e-3).to(input_dtype)
+    cache.append_kv(blocks, offsets, ks, vs)
+    keep = t.ones(tokens, dtype=t.bool, device="cuda")
+    keep[outside] = False
+    b, o = blocks[keep].long(), offsets[keep].long()
+    for x, codes, scales in ((ks, cache.k, cache.k_scales), (vs, cache.v, cache.v_scales)):
+        got_codes = codes[b, o].view(t.uint8).cpu().numpy()
+        got_scales = scales[b, o].cpu().numpy()
+        want_codes, want_scales = oracle.quantize(x[keep].float().cpu().numpy())
+        assert np.array_equal(got_scales.view(np.uint32), want_scales.view(np.uint32))
+        assert np.array_equal(got_codes, want_codes), f"{(got_codes != want_codes).sum()} codes differ"
+    written = t.zeros(num_blocks, 16, dtype=t.bool, device="cuda")
+    written[b, o] = True
+    assert (cache.k.view(t.uint8)[~written] == 0x5A).all()
+    assert (cache.k_scales[~written] == -1.0).all()
+
+
+@t.inference_mode()
 @pytest.mark.parametrize("input_dtype", [t.bfloat16, t.float32])
 def test_fp8_append_large_random_sweep_is_bit_exact(input_dtype):
     # 262144 rows over 16 decades of magnitude: every division and rounding path.
