@@ -809,9 +809,11 @@ decode_mfma_kernel(MfmaArgs a) {
             st.m = kNegInf;
             st.l = 0.0f;
 
-            // Load pipeline: e4m3fn keeps the loads of steps T + 2 and T + 4 in
-            // flight while step T is computed (three buffers); bf16 steps are twice
-            // the bytes and keep one step in flight (two buffers).
+            // Load pipeline: e4m3fn issues the loads of step T + 4 right after step T
+            // is computed, into the buffer step T - 2 used (three buffers), so step
+            // T + 2 is in flight while T is computed and two steps while the wave
+            // waits; bf16 steps are twice the bytes and keep one step in flight (two
+            // buffers).
             // Q^T operands of this head's G query heads: loads issued before the
             // first K/V loads, converted after them, so that the first step waits
             // for nothing else.
@@ -848,18 +850,18 @@ decode_mfma_kernel(MfmaArgs a) {
             };
             if constexpr (ES == 1) {
                 while (true) {
-                    if (T + 4 < t1) issue(buf2, T + 4, r2a, r2b);
                     compute(buf0, T, r0a, r0b);
+                    if (T + 4 < t1) issue(buf2, T + 4, r2a, r2b);
                     keep_pace();
                     T += 2;
                     if (T >= t1) break;
-                    if (T + 4 < t1) issue(buf0, T + 4, r0a, r0b);
                     compute(buf1, T, r1a, r1b);
+                    if (T + 4 < t1) issue(buf0, T + 4, r0a, r0b);
                     keep_pace();
                     T += 2;
                     if (T >= t1) break;
-                    if (T + 4 < t1) issue(buf1, T + 4, r1a, r1b);
                     compute(buf2, T, r2a, r2b);
+                    if (T + 4 < t1) issue(buf1, T + 4, r1a, r1b);
                     keep_pace();
                     T += 2;
                     if (T >= t1) break;
