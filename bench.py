@@ -425,7 +425,7 @@ def _time_decode(caches, q, context, steps: int):
 
 def _misaligned(cache):
     """The same cache with its K and V codes copied 4 bytes past a 16-byte boundary:
-    the MFMA kernel needs 16-byte aligned caches, so decode takes the generic VALU
+    the MFMA kernel needs 16-byte aligned caches, so decode takes the grouped VALU
     kernel (with its 4-byte loads) on identical bytes (scales and table unchanged)."""
     import types
 
@@ -449,8 +449,8 @@ def kernel_legs(steps: int):
         its FP8 tests) at the north-star shape and cfg2, on the same MFMA kernel;
       * f16 (with f16 q, on the MFMA kernel) and f32 (grouped VALU kernel) caches at the
         north-star shape;
-      * MFMA against the generic VALU kernel on the same FP8 bytes (north, cfg4);
-      * the generic kernel at head size 80, a shape the MFMA kernel does not take."""
+      * MFMA against the grouped VALU kernel on the same FP8 bytes (north, cfg4);
+      * the grouped kernel at head size 80, a shape the MFMA kernel does not take."""
     import torch as t
     import oracle
     from aiproj_amd import workloads
@@ -512,19 +512,19 @@ def kernel_legs(steps: int):
             shifted = [_misaligned(c) for c in caches]
             del caches
             t.cuda.empty_cache()
-            generic = _time_decode(shifted, w.q, ctx, max(4, steps // 4))
+            grouped = _time_decode(shifted, w.q, ctx, max(4, steps // 4))
             legs[f"fp8_{name}_mfma"] = entry(spec, 1, *mfma, "decode_mfma_kernel + combine_mfma_kernel")
-            legs[f"fp8_{name}_valu"] = entry(spec, 1, *generic, "decode_split_generic + decode_combine")
+            legs[f"fp8_{name}_valu"] = entry(spec, 1, *grouped, "decode_split_grouped + decode_combine")
             log(f"[A/B {name}] MFMA split {mfma[0]:.1f} / call {mfma[1]:.1f} us; "
-                f"VALU split {generic[0]:.1f} / call {generic[1]:.1f} us")
+                f"VALU split {grouped[0]:.1f} / call {grouped[1]:.1f} us")
             del shifted
             t.cuda.empty_cache()
         spec = workloads.WorkloadSpec("d80", 32, 32, 8, 80, [4096] * 32, seed=2)
         w = workloads.build(spec, "cuda")
         caches = pools_for(w, t.float8_e4m3fn, spec)
         split_us, call_us = _time_decode(caches, w.q, workloads.make_context(w), max(4, steps // 4))
-        legs["fp8_d80_valu"] = entry(spec, 1, split_us, call_us, "decode_split_generic + decode_combine (D 80)")
-        log(f"[generic D80] split {split_us:.1f} us, split + combine {call_us:.1f} us")
+        legs["fp8_d80_valu"] = entry(spec, 1, split_us, call_us, "decode_split_grouped + decode_combine (D 80)")
+        log(f"[grouped D80] split {split_us:.1f} us, split + combine {call_us:.1f} us")
         del caches
         t.cuda.empty_cache()
     return legs
