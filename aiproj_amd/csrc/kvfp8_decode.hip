@@ -799,8 +799,9 @@ int64_t generic_workspace(const Plan& p, int32_t batch, int32_t hq, int32_t d) {
     return (int64_t)(2 * align256(states * sizeof(float)) + align256(states * d * sizeof(float)));
 }
 
-// The MFMA path falls back to the generic kernel when a pointer is not 16-byte
-// aligned, so the size quoted from shapes alone covers both.
+// The MFMA path falls back to the vector-ALU kernels (grouped or generic, which
+// share this workspace layout) when a pointer is not 16-byte aligned, so the size
+// quoted from shapes alone covers every kernel the call may take.
 int64_t workspace_for(const Plan& p, int32_t batch, int32_t hq, int32_t hkv, int32_t d) {
     int64_t need = generic_workspace(p, batch, hq, d);
     if (p.mfma) {
