@@ -1,8 +1,8 @@
 // FP8 paged decode attention on the gfx950 matrix cores.
 //
 // Replaces the Triton split and reduction kernels of reference
-// src/torch_llm/kernals/decode_attention.py:194-550 for e4m3fn caches with
-// D in {64, 128} and pages of 16k tokens.
+// src/torch_llm/kernals/decode_attention.py:194-550 for e4m3fn and bf16 caches
+// (and f16 caches read with f16 q) with D in {64, 128} and pages of 16k tokens.
 //
 // Work split. The attended tokens of the batch form one list of 16-token tiles
 // (sequence by sequence, tile prefix built in LDS from context_lengths, no host
