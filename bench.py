@@ -35,6 +35,9 @@ PEAK_HBM_GBS = 8000.0
 PEAK_BF16_TFLOPS = 2500.0     # dense bf16 MFMA
 MALL_BYTES = 256 * 2 ** 20
 MAX_POOLS = 64
+# Steps per HIP graph: the decode step of a 32-layer model (Llama-3-8B, whose attention shape
+# the north star and cfg2 name) is one graph holding one attention step per layer.
+LAYERS_PER_GRAPH = 32
 
 
 def log(*args):
@@ -107,12 +110,13 @@ class Setup:
         return decode_attention_wrapper(self.w.q, cache, self.context)
 
     def capture(self, steps: int):
-        """HIP graphs holding whole steps (the append and the decode), one step per pool
-        in pool order, as a multi-layer model captures its decode step (each layer on
-        its own cache; the cfg5 leg captures all 16 layers the same way). Returns
-        (graph of num_pools steps, graph of steps % num_pools steps or None): replaying
-        the first steps // num_pools times and the second once runs exactly `steps`
-        steps."""
+        """HIP graphs holding whole steps (the append and the decode), as a multi-layer
+        model captures its decode step: LAYERS_PER_GRAPH steps per graph, step i on cache
+        pool i % num_pools (each layer on its own cache; the pools together exceed twice
+        the last-level cache, so no step finds its cache resident; the cfg5 leg captures
+        all 16 layers of its model the same way). Returns (graph of LAYERS_PER_GRAPH
+        steps, graph of steps % LAYERS_PER_GRAPH steps or None): replaying the first
+        steps // LAYERS_PER_GRAPH times and the second once runs exactly `steps` steps."""
         import torch as t
 
         def graph_of(n):
@@ -122,8 +126,8 @@ class Setup:
                     self.step(i)
             return g
 
-        full = graph_of(self.num_pools)
-        rest = steps % self.num_pools
+        full = graph_of(LAYERS_PER_GRAPH)
+        rest = steps % LAYERS_PER_GRAPH
         tail = graph_of(rest) if rest else None
         t.cuda.synchronize()
         return full, tail
@@ -143,8 +147,8 @@ class _NoGC:
 
 def time_steps(setup: Setup, steps: int, warmup: int):
     """Four timed regions of `steps` calls each, after `warmup` eager steps:
-      * graph replay of whole steps, num_pools steps per graph (no host work between
-        steps, one graph launch per num_pools steps): ms per step, for the step as
+      * graph replay of whole steps, LAYERS_PER_GRAPH steps per graph (no host work
+        between steps, one graph launch per model step): ms per step, for the step as
         the two separate calls and as the fused call;
       * the split (decode) kernel alone, `steps` launches back to back on the
         current stream between two HIP events, pools rotating: its mean launch
@@ -172,7 +176,7 @@ def time_steps(setup: Setup, steps: int, warmup: int):
         t.cuda.synchronize()
         with _NoGC():
             start.record()
-            for _ in range(steps // setup.num_pools):
+            for _ in range(steps // LAYERS_PER_GRAPH):
                 full.replay()
             if tail is not None:
                 tail.replay()
@@ -887,9 +891,10 @@ def main():
                          f"(total {s.total_tokens} KV tokens), FP8 e4m3fn paged cache with per-(page slot, "
                          f"kv head) scales, shuffled page pool; step = 1-token quantized append + decode, "
                          f"the append done by the decode kernel (kvfp8_append_paged_decode)"),
-            "timing": (f"steps replayed from HIP graphs of {main_result['pools']} steps, one per cache pool "
-                       "(as a multi-layer model's decode step graph holds one step per layer); "
-                       "separate_ms_per_step: the same step as the two calls append_kv + decode"),
+            "timing": (f"steps replayed from HIP graphs of {LAYERS_PER_GRAPH} steps, the decode step of a "
+                       f"{LAYERS_PER_GRAPH}-layer model (Llama-3-8B) with one attention step per layer, the layers "
+                       f"cycling through {main_result['pools']} cache pools (together over twice the 256 MB "
+                       "last-level cache); separate_ms_per_step: the same step as the two calls append_kv + decode"),
             "pools_rotated": main_result["pools"],
             "pool_mb": round(main_result["pool_mb"], 1),
         },
