@@ -10,6 +10,7 @@ import os
 import shutil
 import subprocess
 import sys
+import sysconfig
 from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
@@ -17,6 +18,9 @@ PACKAGE_DIR = Path(__file__).resolve().parent
 CSRC = PACKAGE_DIR / "csrc"
 LIBRARY = PACKAGE_DIR / "libkvfp8.so"
 OBJ_DIR = PACKAGE_DIR / "_build"
+# Fast-call Python bindings of the per-step entry points (csrc/pyfast.c), a CPython
+# extension linked to LIBRARY; _native falls back to ctypes where it is absent.
+FAST_EXT = PACKAGE_DIR / ("_kvfp8_fast" + (sysconfig.get_config_var("EXT_SUFFIX") or ".so"))
 
 ARCH = "gfx950"
 
@@ -71,7 +75,26 @@ def build(verbose: bool = False) -> Path:
     os.replace(tmp, LIBRARY)
     if verbose:
         print(f"built {LIBRARY}")
+    build_fast_ext(verbose)
     return LIBRARY
+
+
+def build_fast_ext(verbose: bool = False) -> Path:
+    """Compile csrc/pyfast.c into the CPython extension FAST_EXT, linked to libkvfp8.so
+    in the same directory (found at run time through an $ORIGIN rpath)."""
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        raise RuntimeError("no host C compiler for the fast-call extension")
+    tmp = FAST_EXT.with_suffix(".tmp")
+    cmd = [cc, "-O2", "-shared", "-fPIC", "-Wall", f"-I{sysconfig.get_paths()['include']}",
+           str(CSRC / "pyfast.c"), f"-L{PACKAGE_DIR}", "-lkvfp8", "-Wl,-rpath,$ORIGIN", "-o", str(tmp)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"fast-call extension failed:\n{proc.stdout}\n{proc.stderr}")
+    os.replace(tmp, FAST_EXT)
+    if verbose:
+        print(f"built {FAST_EXT}")
+    return FAST_EXT
 
 
 if __name__ == "__main__":

@@ -82,13 +82,13 @@ class DecodeCall:
     keep: tuple = ()          # every tensor whose address is in `args`
 
     def run(self) -> None:
-        _native.check(_native.lib().kvfp8_paged_decode(*self.args), "kvfp8_paged_decode")
+        _native.check(_native.fn("kvfp8_paged_decode")(*self.args), "kvfp8_paged_decode")
 
     def split(self) -> None:
-        _native.check(_native.lib().kvfp8_paged_decode_split(*self.args), "kvfp8_paged_decode_split")
+        _native.check(_native.fn("kvfp8_paged_decode_split")(*self.args), "kvfp8_paged_decode_split")
 
     def reduce(self) -> None:
-        _native.check(_native.lib().kvfp8_paged_decode_reduce(*self.args), "kvfp8_paged_decode_reduce")
+        _native.check(_native.fn("kvfp8_paged_decode_reduce")(*self.args), "kvfp8_paged_decode_reduce")
 
 
 @functools.lru_cache(maxsize=256)
@@ -221,7 +221,7 @@ def append_decode_attention(q, ks, vs, paged_kv_cache, cache_batch_context):
     if vs.stride(2) != 1 or vs.stride(1) != d:
         vs = vs.contiguous()
     blocks, offsets = _index_tensor(blocks), _index_tensor(offsets)
-    rc = _native.lib().kvfp8_append_paged_decode(
+    rc = _native.fn("kvfp8_append_paged_decode")(
         *call.args, ks.data_ptr(), vs.data_ptr(), _native.dtype_code(ks.dtype),
         ks.stride(0), ks.stride(1), vs.stride(0), vs.stride(1),
         blocks.data_ptr(), _native.dtype_code(blocks.dtype), offsets.data_ptr(), _native.dtype_code(offsets.dtype))

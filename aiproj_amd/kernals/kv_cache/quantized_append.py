@@ -64,8 +64,7 @@ def quantize_append_wrapper(
         return
     ks, vs = _same_dtype(_prepare_input(ks), _prepare_input(vs))
 
-    lib = _native.lib()
-    rc = lib.kvfp8_quantize_append(
+    rc = _native.fn("kvfp8_quantize_append")(
         ks.data_ptr(), vs.data_ptr(), _native.dtype_code(ks.dtype),
         ks.stride(0), ks.stride(1), vs.stride(0), vs.stride(1),
         physical_blocks.data_ptr(), _native.dtype_code(physical_blocks.dtype),
@@ -99,8 +98,7 @@ def store_rows(k_cache, v_cache, ks, vs, rows, cols, what="store_rows"):
     if num_tokens == 0:
         return
     ks, vs = _same_dtype(_prepare_input(ks), _prepare_input(vs))
-    lib = _native.lib()
-    rc = lib.kvfp8_store_append(
+    rc = _native.fn("kvfp8_store_append")(
         ks.data_ptr(), vs.data_ptr(), _native.dtype_code(ks.dtype),
         ks.stride(0), ks.stride(1), vs.stride(0), vs.stride(1),
         rows.data_ptr(), _native.dtype_code(rows.dtype),

@@ -242,3 +242,49 @@ def test_fused_append_and_swiglu_argument_checks(lib):
     assert silu(fake, _native.BF16, 4, 8, 15, fake, 8, None) == -2                 # row shorter than 2 n
     assert silu(None, _native.BF16, 4, 8, 16, fake, 8, None) == -4
     assert silu(fake, _native.BF16, 0, 8, 16, fake, 8, None) == 0                  # nothing to do
+
+
+def test_fast_bindings_match_ctypes_on_host_checks(lib):
+    """The fast-call extension's entry points return what the ctypes ones return for the
+    same arguments (every call below fails a host check, so nothing launches), reject a
+    wrong argument count, and are what `_native.fn` hands out."""
+    fast = pytest.importorskip("aiproj_amd._kvfp8_fast")
+    fake = 16      # a pointer value that is never dereferenced
+    decode = [fake, _native.BF16, 0, 0, 4, 8, 2, 128, fake, fake, _native.E4M3FN, fake, fake,
+              64, 16, fake, 4, 64, fake, _native.I64, fake, _native.I32, 0.125, fake, fake, 1 << 30, None]
+    decode_cases = []
+    for i, value in ((1, 9), (5, 7), (14, 12), (11, None), (25, 16), (4, 8192), (7, 513), (19, _native.F32)):
+        args = list(decode)
+        args[i] = value
+        decode_cases.append(args)
+    for name in ("kvfp8_paged_decode", "kvfp8_paged_decode_split", "kvfp8_paged_decode_reduce"):
+        for args in decode_cases:
+            assert getattr(fast, name)(*args) == getattr(lib, name)(*args) < 0, (name, args)
+        with pytest.raises(TypeError):
+            getattr(fast, name)(*decode[:-1])
+        assert _native.fn(name) is getattr(fast, name)
+    where = [fake, _native.I64, fake, _native.I32]
+    fused_cases = [
+        decode + [fake, fake, _native.E4M3FN, 256, 128, 256, 128] + where,
+        decode + [fake, fake, _native.BF16, 256, 128, 256, 128, fake, _native.F32, fake, _native.I32],
+        decode + [None, fake, _native.BF16, 256, 128, 256, 128] + where,
+        decode + [fake, fake, _native.BF16, 256, 64, 256, 128] + where,
+    ]
+    for args in fused_cases:
+        assert fast.kvfp8_append_paged_decode(*args) == lib.kvfp8_append_paged_decode(*args) < 0
+    append = [fake, fake, _native.BF16, 0, 0, 0, 0, fake, _native.I32, fake, _native.I32,
+              1, 2, 64, 4, 16, fake, fake, fake, fake, None]
+    for i, value in ((8, _native.F32), (2, _native.E4M3FN), (18, None), (12, 0)):
+        args = list(append)
+        args[i] = value
+        assert fast.kvfp8_quantize_append(*args) == lib.kvfp8_quantize_append(*args) < 0, args
+    empty = list(append)
+    empty[11] = 0
+    assert fast.kvfp8_quantize_append(*empty) == lib.kvfp8_quantize_append(*empty) == 0
+    store = append[:18] + [_native.BF16, None]
+    for i, value in ((8, _native.F32), (18, _native.E4M3FN), (0, None)):
+        args = list(store)
+        args[i] = value
+        assert fast.kvfp8_store_append(*args) == lib.kvfp8_store_append(*args) < 0, args
+    with pytest.raises(TypeError):
+        fast.kvfp8_quantize_append(*append, 0)
