@@ -7,6 +7,8 @@ of every sequence over its whole context (reference call site
 `src/torch_llm/model/attention.py:86-99`). Inputs are synthetic and resident in HBM
 before timing starts. Independent cache pools are rotated step to step so their
 total exceeds twice the 256 MB Infinity Cache: every step reads its KV from HBM.
+The timed steps are replayed from HIP graphs of 32 steps, the decode step of a
+32-layer model (Llama-3-8B) with one attention step per layer.
 
 Default workload ("north"): B=32, 32 q / 8 KV heads, D=128, page 16, every
 context 4096 tokens, e4m3fn cache, bf16 q (the metric's "B=32 4k ctx"). The
