@@ -721,8 +721,9 @@ prefill_fa_kernel(PrefillArgs a, int32_t units, int32_t upx, int32_t per_xcd) {
         }
     };
 
-    // A block's work is three phases: qk (S^T = K Q^T, matrix cores), softmax
-    // (vector ALU) and pv (O^T += V^T P^T, matrix cores). The buffer index is a
+    // A block's work is qk (S^T = K Q^T, matrix cores), then softmax_pv: the softmax
+    // (vector ALU) and pv (O^T += V^T P^T, matrix cores), overlapped over the two key
+    // halves. The buffer index is a
     // compile-time constant in every call (the block loop is unrolled by kFaBufs),
     // so all LDS operand addresses are a per-lane offset plus an immediate.
     f32x4_t sacc[4][kFaTiles];
@@ -742,7 +743,16 @@ prefill_fa_kernel(PrefillArgs a, int32_t units, int32_t upx, int32_t per_xcd) {
             }
         }
     };
-    auto softmax = [&](int kb, int L) __attribute__((always_inline)) {
+    // Softmax and PV of one block, in three parts. (1) Per row tile: the mask, the
+    // max test and the rare rescale (the only branches). (2) The probabilities of
+    // keys 0..31, packed into the P^T operands of the first key half. (3) The PV
+    // products of that half, with the probabilities of keys 32..63 computed between
+    // them (one score per row tile and product pair: straight-line code, so the vector
+    // ALU works while the matrix core runs), then the PV products of the second half.
+    // V^T operands come straight from the transposing reads: half h of pair pp covers
+    // the keys of tile 2 pp + h; each operand feeds both row tiles.
+    auto softmax_pv = [&](int kb, int L, auto buf_c) __attribute__((always_inline)) {
+        constexpr int buf = decltype(buf_c)::value;
         const bool full = kb * kKeys + kKeys - 1 <= qa && kb * kKeys + kKeys <= L;   // wave-uniform
 #pragma unroll
         for (int qt = 0; qt < kFaTiles; ++qt) {
@@ -776,39 +786,49 @@ prefill_fa_kernel(PrefillArgs a, int32_t units, int32_t upx, int32_t per_xcd) {
                 m[qt] = m_new;
                 neg_m[qt] = -m_use;
             }
-            float pr[16];
+        }
+        float pr[kFaTiles][16];
+        auto prob = [&](int qt, int i) __attribute__((always_inline)) {
+            pr[qt][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[i / 4][qt][i % 4], a.scale_log2, neg_m[qt]));
+            l[qt] += pr[qt][i];
+        };
+        auto pack_half = [&](int pp) __attribute__((always_inline)) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                pr[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[i / 4][qt][i % 4], a.scale_log2, neg_m[qt]));
-                l[qt] += pr[i];
+            for (int qt = 0; qt < kFaTiles; ++qt)
+#pragma unroll
+                for (int w = 0; w < 4; ++w)
+                    pop[qt][pp][w] = pack2<kF16>(pr[qt][8 * pp + 2 * w], pr[qt][8 * pp + 2 * w + 1]);
+        };
+        auto pv_pair = [&](int pp, int nb) __attribute__((always_inline)) {
+            u32x4_t av;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const s16x4_t x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (lds_s16x4*)(v_lds + buf * (kKeys * ROW) + 16 * (2 * pp + h) * ROW + vt_off[nb]));
+                const uint2 w = __builtin_bit_cast(uint2, x);
+                av[2 * h] = w.x;
+                av[2 * h + 1] = w.y;
             }
 #pragma unroll
-            for (int pp = 0; pp < 2; ++pp)
+            for (int qt = 0; qt < kFaTiles; ++qt) o[qt][nb] = mma16<kF16>(av, pop[qt][pp], o[qt][nb]);
+        };
 #pragma unroll
-                for (int w = 0; w < 4; ++w) pop[qt][pp][w] = pack2<kF16>(pr[8 * pp + 2 * w], pr[8 * pp + 2 * w + 1]);
+        for (int qt = 0; qt < kFaTiles; ++qt)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) prob(qt, i);
+        pack_half(0);
+        constexpr int kPerPair = 8 / NB;     // second-half scores per row tile and product pair
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            pv_pair(0, nb);
+#pragma unroll
+            for (int qt = 0; qt < kFaTiles; ++qt)
+#pragma unroll
+                for (int u = 0; u < kPerPair; ++u) prob(qt, 8 + kPerPair * nb + u);
         }
-    };
-    // V^T operands straight from the transposing reads: half h of pair pp covers the
-    // keys of tile 2 pp + h. Each operand feeds both row tiles.
-    auto pv = [&](auto buf_c) __attribute__((always_inline)) {
-        constexpr int buf = decltype(buf_c)::value;
+        pack_half(1);
 #pragma unroll
-        for (int pp = 0; pp < 2; ++pp) {
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb) {
-                u32x4_t av;
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const s16x4_t x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (lds_s16x4*)(v_lds + buf * (kKeys * ROW) + 16 * (2 * pp + h) * ROW + vt_off[nb]));
-                    const uint2 w = __builtin_bit_cast(uint2, x);
-                    av[2 * h] = w.x;
-                    av[2 * h + 1] = w.y;
-                }
-#pragma unroll
-                for (int qt = 0; qt < kFaTiles; ++qt) o[qt][nb] = mma16<kF16>(av, pop[qt][pp], o[qt][nb]);
-            }
-        }
+        for (int nb = 0; nb < NB; ++nb) pv_pair(1, nb);
     };
     // Normalize and store the current item's rows: lane (row, j) holds dims
     // 16 nb + 4 j + jj of its row (tile nb of the V^T operand covers dims 16 nb ..).
@@ -859,10 +879,7 @@ prefill_fa_kernel(PrefillArgs a, int32_t units, int32_t upx, int32_t per_xcd) {
         if (compute) qk(buf_c);
         const bool loaded = load_next((buf + 2) % kFaBufs);
         if (next) load_q(ni);
-        if (compute) {
-            softmax(ckb, ci.L);
-            pv(buf_c);
-        }
+        if (compute) softmax_pv(ckb, ci.L, buf_c);
         if (loaded) {
             if (next) __builtin_amdgcn_s_waitcnt(kWBoth);
             else __builtin_amdgcn_s_waitcnt(kWBlock);
