@@ -706,7 +706,7 @@ __device__ __forceinline__ void put_new_token(const MfmaArgs& a, const NewRow<C>
     }
 }
 
-template <int C, int QT, int ES, int kSets, bool kAppend, bool kF16>
+template <int C, int QT, int ES, int kSets, bool kAppend, bool kF16, bool kRep>
 __global__ void __launch_bounds__(kMaxThreads)
 decode_mfma_kernel(MfmaArgs a) {
     constexpr int D = 64 * C;
@@ -772,7 +772,16 @@ decode_mfma_kernel(MfmaArgs a) {
         else __builtin_amdgcn_s_setprio(0);
     };
 
-    for (int h = wave; h < a.d.num_kv_heads; h += waves) {
+    // Fewer than 8 KV heads (a divisor of 8; kRep): the workgroup still has 8 waves,
+    // R = 8 / Hkv replicas per head. Replica r of a head takes steps r, r + R, r + 2R,
+    // ... of every segment, and at the segment's end the replicas merge their
+    // softmax states through LDS into replica 0, which stores. A CU then streams
+    // with two waves per SIMD instead of one.
+    const int hw = kRep ? a.d.num_kv_heads : waves;        // heads served at a time
+    const int rep_r = kRep ? wave / hw : 0;                   // this wave's replica
+    const int reps = kRep ? waves / hw : 1;
+    const int dT = 2 * reps;                                  // tiles between this wave's steps
+    for (int h = kRep ? wave - rep_r * hw : wave; h < a.d.num_kv_heads; h += hw) {
         int32_t tile = start;
         int b = uniform(find_seq(prefix, a.d.batch, tile));
         while (tile < end) {
@@ -793,12 +802,14 @@ decode_mfma_kernel(MfmaArgs a) {
             // sequence's new token. Its loads go out first; the quantized row is
             // stored before the loads of the tile that holds it (after the first
             // issued steps when that tile is not among them).
-            const bool append = kAppend && seg1 == seq1;
+            // With replicas, the one whose steps include the last tile writes.
+            const bool append = kAppend && seg1 == seq1 && (!kRep || ((t1 - 1 - t0) >> 1) % reps == rep_r);
             NewRow<C> fresh;
             if constexpr (kAppend) {
                 if (append) fetch_new_token<C>(a, b, h, lane, fresh);
             }
-            const bool put_early = t1 - 1 < t0 + (ES == 1 ? 4 : 2);
+            const int32_t T0 = t0 + 2 * rep_r;     // this wave's first step
+            const bool put_early = t1 - 1 < T0 + (ES == 1 ? 2 * dT : 2);
             if constexpr (kAppend) {
                 if (append && put_early) put_new_token<C>(a, fresh, lane);
             }
@@ -830,10 +841,10 @@ decode_mfma_kernel(MfmaArgs a) {
                 rb = tile0 + 1 < t1 ? tile_ref(a, table_row, tile0 + 1) : TileRef{0, 0};
                 load_step<C, ES>(dst, a, h, ra, rb, lane);
             };
-            int32_t T = t0;
-            issue(buf0, T, r0a, r0b);
+            int32_t T = T0;
+            if (!kRep || T < t1) issue(buf0, T, r0a, r0b);
             if constexpr (ES == 1) {
-                if (T + 2 < t1) issue(buf1, T + 2, r1a, r1b);
+                if (T + dT < t1) issue(buf1, T + dT, r1a, r1b);
             }
             if constexpr (kAppend) {
                 if (append && !put_early) put_new_token<C>(a, fresh, lane);
@@ -849,42 +860,79 @@ decode_mfma_kernel(MfmaArgs a) {
                 compute_step<C, ES, kHiLo, kSets, kF16>(st, cur, qh, ql, stage, lane, lim_a, lim_b, a.d.score_scale);
             };
             if constexpr (ES == 1) {
-                while (true) {
+                while (!kRep || T < t1) {
                     compute(buf0, T, r0a, r0b);
-                    if (T + 4 < t1) issue(buf2, T + 4, r2a, r2b);
+                    if (T + 2 * dT < t1) issue(buf2, T + 2 * dT, r2a, r2b);
                     keep_pace();
-                    T += 2;
+                    T += dT;
                     if (T >= t1) break;
                     compute(buf1, T, r1a, r1b);
-                    if (T + 4 < t1) issue(buf0, T + 4, r0a, r0b);
+                    if (T + 2 * dT < t1) issue(buf0, T + 2 * dT, r0a, r0b);
                     keep_pace();
-                    T += 2;
+                    T += dT;
                     if (T >= t1) break;
                     compute(buf2, T, r2a, r2b);
-                    if (T + 4 < t1) issue(buf1, T + 4, r1a, r1b);
+                    if (T + 2 * dT < t1) issue(buf1, T + 2 * dT, r1a, r1b);
                     keep_pace();
-                    T += 2;
+                    T += dT;
                     if (T >= t1) break;
                 }
             } else {
-                while (true) {
-                    if (T + 2 < t1) issue(buf1, T + 2, r1a, r1b);
+                while (!kRep || T < t1) {
+                    if (T + dT < t1) issue(buf1, T + dT, r1a, r1b);
                     compute(buf0, T, r0a, r0b);
                     keep_pace();
-                    T += 2;
+                    T += dT;
                     if (T >= t1) break;
-                    if (T + 2 < t1) issue(buf0, T + 2, r0a, r0b);
+                    if (T + dT < t1) issue(buf0, T + dT, r0a, r0b);
                     compute(buf1, T, r1a, r1b);
                     keep_pace();
-                    T += 2;
+                    T += dT;
                     if (T >= t1) break;
+                }
+            }
+            if constexpr (kRep) {
+                // Tree merge of the replicas' softmax states into replica 0: in each
+                // round replicas [half, 2 half) publish (structure of arrays, one float
+                // per lane and value: conflict-free) and replica r < half merges that
+                // of r + half. The second barrier keeps the next publications behind
+                // the merge. At most 4 states are published at a time.
+                constexpr int kVals = 4 * NB + 2;
+                float* merge = reinterpret_cast<float*>(meta + a.d.batch);   // after the metadata
+                for (int half = reps >> 1; half > 0; half >>= 1) {
+                    if (rep_r >= half && rep_r < 2 * half) {
+                        float* mine = merge + ((rep_r - half) * hw + h) * (kVals * 64);
+#pragma unroll
+                        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                            for (int jj = 0; jj < 4; ++jj) mine[(4 * nb + jj) * 64 + lane] = st.o[nb][jj];
+                        mine[(4 * NB) * 64 + lane] = st.m;
+                        mine[(4 * NB + 1) * 64 + lane] = st.l;
+                    }
+                    __syncthreads();
+                    if (rep_r < half) {
+                        const float* other = merge + (rep_r * hw + h) * (kVals * 64);
+                        const float mo = other[(4 * NB) * 64 + lane];
+                        const float lo = other[(4 * NB + 1) * 64 + lane];
+                        const float mn = fmaxf(st.m, mo);
+                        const float mu = mn == kNegInf ? 0.0f : mn;
+                        const float sa = fast_exp2(st.m - mu), sb = fast_exp2(mo - mu);
+#pragma unroll
+                        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                            for (int jj = 0; jj < 4; ++jj)
+                                st.o[nb][jj] = st.o[nb][jj] * sa + other[(4 * nb + jj) * 64 + lane] * sb;
+                        st.l = st.l * sa + lo * sb;
+                        st.m = mn;
+                    }
+                    __syncthreads();
                 }
             }
 
             // Denominator: sum the four lane groups of each column.
             float lt = st.l + __shfl_xor(st.l, 16);
             lt += __shfl_xor(lt, 32);
-            if (qlive) {
+            if (qlive && rep_r == 0) {
                 if (whole) {
                     const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
 #pragma unroll
@@ -1021,7 +1069,20 @@ int ilog2(int64_t x) {
     return s;
 }
 
+// Waves that serve distinct KV heads: one per head, up to kMaxWaves.
 int waves_for(int32_t num_kv_heads) { return num_kv_heads < kMaxWaves ? num_kv_heads : kMaxWaves; }
+
+// Fewer KV heads than kMaxWaves, dividing it: the workgroup runs kMaxWaves waves, R =
+// kMaxWaves / heads replicas of each head (kRep), when the replicas' merge buffer fits
+// in LDS beside the batch-sized tables.
+constexpr size_t kMaxGroupLds = 64 * 1024;
+template <int C>
+constexpr size_t replica_merge_bytes() { return (size_t)(kMaxWaves / 2) * (4 * (4 * C) + 2) * 64 * sizeof(float); }
+template <int C>
+bool replicated(int32_t num_kv_heads, size_t table_lds) {
+    return num_kv_heads < kMaxWaves && kMaxWaves % num_kv_heads == 0 &&
+           table_lds + replica_merge_bytes<C>() <= kMaxGroupLds;
+}
 
 // Compute units of the current device (cached per device id).
 int device_cus() {
@@ -1041,21 +1102,21 @@ int64_t max_groups(int32_t num_kv_heads) {
     return (int64_t)device_cus() * (per_cu > 0 ? per_cu : 1);
 }
 
-template <int C, int QT, int ES, int kSets, bool kAppend = false, bool kF16 = false>
-hipError_t launch_c(const MfmaArgs& a, int64_t cap, hipStream_t s, int phases) {
-    const int threads = 64 * waves_for(a.d.num_kv_heads);
-    const size_t lds = (size_t)(2 * a.d.batch + 1) * sizeof(int32_t);
+template <int C, int QT, int ES, int kSets, bool kAppend, bool kF16, bool kRep>
+hipError_t launch_w(const MfmaArgs& a, int64_t cap, hipStream_t s, int phases) {
+    const int threads = 64 * (kRep ? kMaxWaves : waves_for(a.d.num_kv_heads));
+    const size_t lds = (size_t)(2 * a.d.batch + 1) * sizeof(int32_t) + (kRep ? replica_merge_bytes<C>() : 0);
     // Resident workgroups per CU: the register limit, queried once per (device,
-    // workgroup size) without dynamic LDS, capped by what the batch-sized LDS
-    // (up to 64 KiB) leaves room for. Only a sizing choice: the work split is
-    // correct for any grid.
+    // workgroup size) without dynamic LDS, capped by what the dynamic LDS (batch-sized
+    // tables, replica merge buffer; up to 64 KiB) leaves room for. Only a sizing
+    // choice: the work split is correct for any grid.
     static int resident[64][kMaxWaves + 1] = {};     // per template instance
     static int lds_per_cu[64] = {};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
     int& per_cu = resident[dev][threads / 64];
     if (per_cu == 0) {
-        const void* fn = reinterpret_cast<const void*>(&decode_mfma_kernel<C, QT, ES, kSets, kAppend, kF16>);
+        const void* fn = reinterpret_cast<const void*>(&decode_mfma_kernel<C, QT, ES, kSets, kAppend, kF16, kRep>);
         int n = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, threads, 0) != hipSuccess || n <= 0) n = 1;
         per_cu = n;
@@ -1071,14 +1132,22 @@ hipError_t launch_c(const MfmaArgs& a, int64_t cap, hipStream_t s, int phases) {
     int64_t groups = (int64_t)device_cus() * (fit > 0 ? fit : 1);
     groups = groups < cap ? groups : cap;
     if (phases & kPhaseSplit) {
-        const hipError_t err = launch_timed(decode_mfma_kernel<C, QT, ES, kSets, kAppend, kF16>, dim3((unsigned)groups), dim3(threads),
-                                            lds, s, next_kernel_timing(), a);
+        const hipError_t err =
+            launch_timed(decode_mfma_kernel<C, QT, ES, kSets, kAppend, kF16, kRep>, dim3((unsigned)groups),
+                         dim3(threads), lds, s, next_kernel_timing(), a);
         if (err != hipSuccess) return err;
     }
     if (!(phases & kPhaseReduce)) return hipSuccess;
     const int64_t pairs = (int64_t)a.d.batch * a.d.num_q_heads;
     hipLaunchKernelGGL((combine_mfma_kernel<C, QT>), dim3((unsigned)((pairs + 3) / 4)), dim3(256), 0, s, a);
     return hipGetLastError();
+}
+
+template <int C, int QT, int ES, int kSets, bool kAppend = false, bool kF16 = false>
+hipError_t launch_c(const MfmaArgs& a, int64_t cap, hipStream_t s, int phases) {
+    if (replicated<C>(a.d.num_kv_heads, (size_t)(2 * a.d.batch + 1) * sizeof(int32_t)))
+        return launch_w<C, QT, ES, kSets, kAppend, kF16, true>(a, cap, s, phases);
+    return launch_w<C, QT, ES, kSets, kAppend, kF16, false>(a, cap, s, phases);
 }
 
 }  // namespace

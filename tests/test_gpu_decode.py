@@ -531,6 +531,49 @@ def test_large_batch_with_sixteen_kv_heads():
 
 
 @t.inference_mode()
+@pytest.mark.parametrize("hq,hkv,d,batch,long_len", [
+    (16, 4, 128, 3839, 0),      # the largest batch whose tables leave room for the replicas' merge buffer
+    (16, 4, 128, 3841, 0),      # one table entry over: one wave per head
+    (8, 2, 64, 5887, 0),        # the same boundary at D 64
+    (16, 4, 128, 3, 9000),      # one long sequence cut into many workgroups' pieces
+    (8, 1, 128, 5, 6000),
+    (16, 2, 64, 4, 4100),
+])
+def test_replicated_heads(hq, hkv, d, batch, long_len):
+    """Fewer than 8 KV heads (dividing 8) run 8 waves per workgroup, 8 / Hkv replicas
+    of each head that merge their softmax states at the end of every segment, when
+    the merge buffer fits in LDS beside the batch-sized tables. Both sides of that
+    LDS boundary, and sequences cut into pieces shorter than the replicas' stride
+    (replicas with no step), against float32 dequantize-then-attend and the oracle;
+    split then reduce equals the single call bit for bit."""
+    from aiproj_amd.kernals.decode_attention import prepare_decode
+    from tests.helpers import torch_paged_decode
+
+    lengths = [(i * 53) % 97 + 1 for i in range(batch)]
+    if long_len:
+        lengths[1] = long_len
+    spec = workloads.WorkloadSpec("replicas", batch, hq, hkv, d, lengths, seed=23)
+    w = workloads.build(spec, "cuda")
+    cache = PagedKVCache(w.num_blocks, 16, hkv, d, "cuda", FP8)
+    workloads.fill_cache(w, cache, "cuda")
+    k, v = workloads.new_kv(w, "cuda")
+    cache.append_kv(w.new_blocks, w.new_offsets, k, v)
+    ctx = workloads.make_context(w)
+    out = decode_attention_wrapper(w.q, cache, ctx)
+    ref = torch_paged_decode(w.q, cache, w.cache_slots, ctx.context_lengths, w.block_table)
+    t.testing.assert_close(out.float(), ref, rtol=NORTH_STAR_RTOL, atol=NORTH_STAR_ATOL)
+    call = prepare_decode(w.q, cache, ctx)
+    call.output.fill_(float("nan"))
+    call.split()
+    call.reduce()
+    assert t.equal(call.output.view(t.int16), out.view(t.int16))
+    rows = sorted({0, 1, batch - 1})
+    expected = oracle_decode(w.q, cache, w.block_table, w.cache_slots, lengths, rows=rows)
+    t.testing.assert_close(out[rows].double().cpu(), t.from_numpy(expected), rtol=NORTH_STAR_RTOL,
+                           atol=NORTH_STAR_ATOL)
+
+
+@t.inference_mode()
 @pytest.mark.parametrize("head_dim", [64, 80])
 def test_maximum_batch(head_dim):
     """8,191 sequences, the most the decode kernels' LDS tile prefix holds (8,192 is
