@@ -580,13 +580,15 @@ prefill_fa_kernel(PrefillArgs a, int32_t units, int32_t upx, int32_t per_xcd) {
     // the layout is the load order: chunk slot c holds row c / CPR, chunk
     // (c % CPR) ^ (row % CPR). The xor spreads the 16 rows that one operand read
     // touches at one column over 16 different chunk positions (bank groups).
-    __shared__ __attribute__((aligned(16))) uint8_t lds_k[kFaBufs][kKeys * ROW];
-    __shared__ __attribute__((aligned(16))) uint8_t lds_v[kFaBufs][kKeys * ROW];
+    // V buffers first, then K buffers (96 KiB at D 128): every V^T operand address is
+    // a per-lane offset plus an immediate below 64 KiB; the K reads take a per-lane
+    // base register that includes the K region's start.
+    __shared__ __attribute__((aligned(16))) uint8_t lds_kv[2 * kFaBufs][kKeys * ROW];
     typedef __attribute__((address_space(3))) void* lds_ptr;
 
     // LDS byte addresses of the K and V buffers (the DMA loads take them in m0).
-    const uint32_t k_lds0 = (uint32_t)(uintptr_t)(lds_ptr)(&lds_k[0][0]);
-    const uint32_t v_lds0 = (uint32_t)(uintptr_t)(lds_ptr)(&lds_v[0][0]);
+    const uint32_t k_lds0 = (uint32_t)(uintptr_t)(lds_ptr)(&lds_kv[kFaBufs][0]);
+    const uint32_t v_lds0 = (uint32_t)(uintptr_t)(lds_ptr)(&lds_kv[0][0]);
 
     FaSchedule sc;
     sc.P = per_xcd;
@@ -685,9 +687,17 @@ prefill_fa_kernel(PrefillArgs a, int32_t units, int32_t upx, int32_t per_xcd) {
     //   4 r + i / 4 (r = 0..3). Lane (j, m16) therefore reads dims 16 nb + 4 (m16 % 4)
     //   .. + 3 of key row 4 j + m16 / 4 of a 16-key tile and receives
     //   V[4 j + r][16 nb + m16]: four keys of its dim, in the P^T operand's key order.
-    int k_off[KS], vt_off[NB];
+    // The K offsets are LDS addresses that include the K region's start, computed in
+    // assembly so that the compiler keeps them as base registers: folded into a
+    // constant, the start plus a buffer's offset exceeds the 16-bit immediate of the
+    // LDS instructions, and every read would take its own address addition.
+    uint32_t k_addr[KS];
+    int vt_off[NB];
 #pragma unroll
-    for (int s = 0; s < KS; ++s) k_off[s] = m16 * ROW + 16 * ((4 * s + j) ^ (m16 % CPR));
+    for (int s = 0; s < KS; ++s) {
+        const uint32_t off = (uint32_t)(m16 * ROW + 16 * ((4 * s + j) ^ (m16 % CPR)));
+        __asm__("v_add_u32 %0, %1, %2" : "=v"(k_addr[s]) : "s"(k_lds0), "v"(off));
+    }
     {
         const int vrow = 4 * j + (m16 >> 2);
 #pragma unroll
@@ -697,7 +707,8 @@ prefill_fa_kernel(PrefillArgs a, int32_t units, int32_t upx, int32_t per_xcd) {
     typedef __attribute__((address_space(3))) const uint8_t lds_u8;
     typedef short s16x4_t __attribute__((ext_vector_type(4)));
     typedef __attribute__((address_space(3))) s16x4_t lds_s16x4;
-    lds_u8* const v_lds = (lds_u8*)(&lds_v[0][0]);
+    typedef __attribute__((address_space(3))) const u32x4_t lds_u32x4;
+    lds_u8* const v_lds = (lds_u8*)(&lds_kv[0][0]);
 
     // Compute state of the current item: accumulators o[qt][nb] for the head dims;
     // l[qt] holds a lane's part (16 of every 64 keys) of its row's float32
@@ -723,20 +734,20 @@ prefill_fa_kernel(PrefillArgs a, int32_t units, int32_t upx, int32_t per_xcd) {
 
     // A block's work is qk (S^T = K Q^T, matrix cores), then softmax_pv: the softmax
     // (vector ALU) and pv (O^T += V^T P^T, matrix cores), overlapped over the two key
-    // halves. The buffer index is a
-    // compile-time constant in every call (the block loop is unrolled by kFaBufs),
-    // so all LDS operand addresses are a per-lane offset plus an immediate.
+    // halves. The buffer index is a compile-time constant in every call (the block
+    // loop is unrolled by kFaBufs), so all LDS operand addresses are a per-lane
+    // register plus an immediate.
     f32x4_t sacc[4][kFaTiles];
     u32x4_t pop[kFaTiles][2];           // P^T operands; pp holds keys 16 (2 pp + i / 4) + 4 j + i % 4
     auto qk = [&](auto buf_c) __attribute__((always_inline)) {
         constexpr int buf = decltype(buf_c)::value;
-        const uint8_t* kl = lds_k[buf];
         // 4 key tiles x 2 row tiles; each K operand feeds both row tiles.
 #pragma unroll
         for (int s = 0; s < KS; ++s) {
+            lds_u8* const kl = (lds_u8*)(uintptr_t)k_addr[s] + buf * (kKeys * ROW);
 #pragma unroll
             for (int kt = 0; kt < 4; ++kt) {
-                const u32x4_t kop = *reinterpret_cast<const u32x4_t*>(kl + 16 * kt * ROW + k_off[s]);
+                const u32x4_t kop = *(lds_u32x4*)(kl + 16 * kt * ROW);
 #pragma unroll
                 for (int qt = 0; qt < kFaTiles; ++qt)
                     sacc[kt][qt] = mma16<kF16>(kop, qop[qt][s], s == 0 ? f32x4_t{0.0f, 0.0f, 0.0f, 0.0f} : sacc[kt][qt]);
