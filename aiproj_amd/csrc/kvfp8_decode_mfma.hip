@@ -1072,18 +1072,6 @@ int ilog2(int64_t x) {
 // Waves that serve distinct KV heads: one per head, up to kMaxWaves.
 int waves_for(int32_t num_kv_heads) { return num_kv_heads < kMaxWaves ? num_kv_heads : kMaxWaves; }
 
-// Fewer KV heads than kMaxWaves, dividing it: the workgroup runs kMaxWaves waves, R =
-// kMaxWaves / heads replicas of each head (kRep), when the replicas' merge buffer fits
-// in LDS beside the batch-sized tables.
-constexpr size_t kMaxGroupLds = 64 * 1024;
-template <int C>
-constexpr size_t replica_merge_bytes() { return (size_t)(kMaxWaves / 2) * (4 * (4 * C) + 2) * 64 * sizeof(float); }
-template <int C>
-bool replicated(int32_t num_kv_heads, size_t table_lds) {
-    return num_kv_heads < kMaxWaves && kMaxWaves % num_kv_heads == 0 &&
-           table_lds + replica_merge_bytes<C>() <= kMaxGroupLds;
-}
-
 // Compute units of the current device (cached per device id).
 int device_cus() {
     static int cus[64] = {0};
@@ -1095,6 +1083,25 @@ int device_cus() {
         cus[dev] = n;
     }
     return cus[dev];
+}
+
+// Fewer KV heads than kMaxWaves, dividing it: the plain decode runs kMaxWaves waves per
+// workgroup, R = kMaxWaves / heads replicas of each head (kRep), when
+//   - the replicas' merge buffer fits in LDS beside the batch-sized tables, and
+//   - the batch can give every replica steps: its tile capacity (batch x table width)
+//     is at least 2 R tiles per CU. Below that most replicas idle and the 8-wave
+//     workgroups measured slower (cfg1: 8.5 against 6.5 us).
+// The fused append + decode kernel keeps one wave per head: with the replicas' merge
+// it spills registers and measured 1.3-2.7 us slower.
+constexpr size_t kMaxGroupLds = 64 * 1024;
+template <int C>
+constexpr size_t replica_merge_bytes() { return (size_t)(kMaxWaves / 2) * (4 * (4 * C) + 2) * 64 * sizeof(float); }
+template <int C>
+bool replicated(const DecodeArgs& d, size_t table_lds) {
+    if (d.num_kv_heads >= kMaxWaves || kMaxWaves % d.num_kv_heads != 0) return false;
+    if (table_lds + replica_merge_bytes<C>() > kMaxGroupLds) return false;
+    const int64_t tiles = (int64_t)d.batch * d.bt_width * (d.block_size / 16);
+    return tiles >= (int64_t)device_cus() * 2 * (kMaxWaves / d.num_kv_heads);
 }
 
 int64_t max_groups(int32_t num_kv_heads) {
@@ -1145,8 +1152,10 @@ hipError_t launch_w(const MfmaArgs& a, int64_t cap, hipStream_t s, int phases) {
 
 template <int C, int QT, int ES, int kSets, bool kAppend = false, bool kF16 = false>
 hipError_t launch_c(const MfmaArgs& a, int64_t cap, hipStream_t s, int phases) {
-    if (replicated<C>(a.d.num_kv_heads, (size_t)(2 * a.d.batch + 1) * sizeof(int32_t)))
-        return launch_w<C, QT, ES, kSets, kAppend, kF16, true>(a, cap, s, phases);
+    if constexpr (!kAppend) {
+        if (replicated<C>(a.d, (size_t)(2 * a.d.batch + 1) * sizeof(int32_t)))
+            return launch_w<C, QT, ES, kSets, kAppend, kF16, true>(a, cap, s, phases);
+    }
     return launch_w<C, QT, ES, kSets, kAppend, kF16, false>(a, cap, s, phases);
 }
 

@@ -531,21 +531,25 @@ def test_large_batch_with_sixteen_kv_heads():
 
 
 @t.inference_mode()
-@pytest.mark.parametrize("hq,hkv,d,batch,long_len", [
-    (16, 4, 128, 3839, 0),      # the largest batch whose tables leave room for the replicas' merge buffer
-    (16, 4, 128, 3841, 0),      # one table entry over: one wave per head
-    (8, 2, 64, 5887, 0),        # the same boundary at D 64
-    (16, 4, 128, 3, 9000),      # one long sequence cut into many workgroups' pieces
-    (8, 1, 128, 5, 6000),
-    (16, 2, 64, 4, 4100),
+@pytest.mark.parametrize("hq,hkv,d,batch,long_len,cache_dtype", [
+    (16, 4, 128, 3839, 0, FP8),      # the largest batch whose tables leave room for the replicas' merge buffer
+    (16, 4, 128, 3841, 0, FP8),      # one table entry over: one wave per head
+    (8, 2, 64, 5887, 0, FP8),        # the same boundary at D 64
+    (16, 4, 128, 3, 9000, FP8),      # one long sequence cut into many workgroups' pieces
+    (8, 1, 128, 12, 6000, FP8),
+    (16, 2, 64, 8, 4100, FP8),
+    (16, 4, 128, 3, 9000, t.bfloat16),
+    (16, 2, 64, 8, 4100, t.bfloat16),
 ])
-def test_replicated_heads(hq, hkv, d, batch, long_len):
+def test_replicated_heads(hq, hkv, d, batch, long_len, cache_dtype):
     """Fewer than 8 KV heads (dividing 8) run 8 waves per workgroup, 8 / Hkv replicas
     of each head that merge their softmax states at the end of every segment, when
-    the merge buffer fits in LDS beside the batch-sized tables. Both sides of that
-    LDS boundary, and sequences cut into pieces shorter than the replicas' stride
-    (replicas with no step), against float32 dequantize-then-attend and the oracle;
-    split then reduce equals the single call bit for bit."""
+    the merge buffer fits in LDS beside the batch-sized tables and the batch's tile
+    capacity (batch x table width) is at least 2 x 8 / Hkv tiles per CU (every case
+    here). Both sides of that LDS boundary, and sequences cut into pieces shorter than
+    the replicas' stride (replicas with no step), against float32
+    dequantize-then-attend and the oracle; split then reduce equals the single call
+    bit for bit."""
     from aiproj_amd.kernals.decode_attention import prepare_decode
     from tests.helpers import torch_paged_decode
 
@@ -554,7 +558,7 @@ def test_replicated_heads(hq, hkv, d, batch, long_len):
         lengths[1] = long_len
     spec = workloads.WorkloadSpec("replicas", batch, hq, hkv, d, lengths, seed=23)
     w = workloads.build(spec, "cuda")
-    cache = PagedKVCache(w.num_blocks, 16, hkv, d, "cuda", FP8)
+    cache = PagedKVCache(w.num_blocks, 16, hkv, d, "cuda", cache_dtype)
     workloads.fill_cache(w, cache, "cuda")
     k, v = workloads.new_kv(w, "cuda")
     cache.append_kv(w.new_blocks, w.new_offsets, k, v)
