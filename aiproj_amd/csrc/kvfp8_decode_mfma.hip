@@ -83,6 +83,15 @@ struct MfmaArgs {
 
 __device__ __forceinline__ int32_t uniform(int32_t x) { return __builtin_amdgcn_readfirstlane(x); }
 
+// floor(n / d) for 0 <= n < 2^53 and d >= 1 through one IEEE double division, in
+// place of the long instruction sequence of a 64-bit integer division. Exact: n and d
+// convert exactly, the quotient q = n / d rounds to within q 2^-53 < 1 / d of itself,
+// and when q is not an integer the next integer above it is at least 1 / d away (an
+// integer q is exact), so the truncation lands on floor(q).
+__device__ __forceinline__ int32_t floor_div(int64_t n, int64_t d) {
+    return (int32_t)((double)n / (double)d);
+}
+
 __device__ __forceinline__ int64_t uniform64(int64_t x) {
     const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int32_t)(uint32_t)x);
     const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int32_t)(uint32_t)((uint64_t)x >> 32));
@@ -731,8 +740,9 @@ decode_mfma_kernel(MfmaArgs a) {
     }
     const int w = blockIdx.x;
     if (w >= groups) return;
-    const int32_t start = (int32_t)((int64_t)w * total / groups);
-    const int32_t end = (int32_t)((int64_t)(w + 1) * total / groups);
+    // w * total < 2^11 * 2^31 (groups <= the grid, tiles < 2^31 on the host).
+    const int32_t start = uniform(floor_div((int64_t)w * total, groups));
+    const int32_t end = uniform(floor_div((int64_t)(w + 1) * total, groups));
 
     const int waves = blockDim.x >> 6;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -977,7 +987,7 @@ __device__ __forceinline__ void store_out4(const DecodeArgs& a, int b, int hq, i
 
 // Workgroup whose tile range holds tile x: the largest w with w W / groups <= x.
 __device__ __forceinline__ int32_t group_of(int64_t x, int64_t total, int64_t groups) {
-    return (int32_t)(((x + 1) * groups - 1) / total);
+    return floor_div((x + 1) * groups - 1, total);     // < 2^42
 }
 
 // Merge of the pieces of every cut sequence (reference decode_attention.py:437-550):
@@ -997,7 +1007,7 @@ combine_mfma_kernel(MfmaArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int64_t pair = (int64_t)blockIdx.x * 4 + wave;
     if (pair >= (int64_t)a.d.batch * a.d.num_q_heads) return;
-    const int b = (int)(pair / a.d.num_q_heads);
+    const int b = uniform(floor_div(pair, a.d.num_q_heads));
     const int hq = (int)(pair - (int64_t)b * a.d.num_q_heads);
     const int32_t t0 = a.plan[b], t1 = a.plan[b + 1];
     const int d4 = lane % kLanesPerPiece, po = lane / kLanesPerPiece;
@@ -1007,7 +1017,7 @@ combine_mfma_kernel(MfmaArgs a) {
     }
     const int64_t total = a.plan[a.d.batch];
     const int64_t groups = a.plan[a.d.batch + 1];
-    const int32_t w0 = group_of(t0, total, groups), w1 = group_of(t1 - 1, total, groups);
+    const int32_t w0 = uniform(group_of(t0, total, groups)), w1 = uniform(group_of(t1 - 1, total, groups));
     if (w0 == w1) return;    // finished by the decode kernel
     const int32_t pieces = w1 - w0 + 1;
     const int64_t hq_count = a.d.num_q_heads;
@@ -1015,7 +1025,7 @@ combine_mfma_kernel(MfmaArgs a) {
     // sequence, so it is their first segment (state 2 w); w0 holds it as its first
     // segment only when its range starts at t0, else as its last (state 2 w + 1).
     // One division per wave instead of one per piece.
-    const int32_t cut0 = (int64_t)w0 * total / groups < t0 ? 1 : 0;
+    const int32_t cut0 = floor_div((int64_t)w0 * total, groups) < t0 ? 1 : 0;
     auto state_index = [&](int32_t i) -> int64_t {
         const int64_t w = w0 + i;
         return (2 * w + (i == 0 ? cut0 : 0)) * hq_count + hq;
