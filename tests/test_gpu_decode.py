@@ -531,17 +531,19 @@ def test_large_batch_with_sixteen_kv_heads():
 
 
 @t.inference_mode()
-@pytest.mark.parametrize("hq,hkv,d,batch,long_len,cache_dtype", [
-    (16, 4, 128, 3839, 0, FP8),      # the largest batch whose tables leave room for the replicas' merge buffer
-    (16, 4, 128, 3841, 0, FP8),      # one table entry over: one wave per head
-    (8, 2, 64, 5887, 0, FP8),        # the same boundary at D 64
-    (16, 4, 128, 3, 9000, FP8),      # one long sequence cut into many workgroups' pieces
-    (8, 1, 128, 12, 6000, FP8),
-    (16, 2, 64, 8, 4100, FP8),
-    (16, 4, 128, 3, 9000, t.bfloat16),
-    (16, 2, 64, 8, 4100, t.bfloat16),
+@pytest.mark.parametrize("hq,hkv,d,batch,long_len,cache_dtype,block_size", [
+    (16, 4, 128, 3839, 0, FP8, 16),      # the largest batch whose tables leave room for the replicas' merge buffer
+    (16, 4, 128, 3841, 0, FP8, 16),      # one table entry over: one wave per head
+    (8, 2, 64, 5887, 0, FP8, 16),        # the same boundary at D 64
+    (16, 4, 128, 3, 9000, FP8, 16),      # one long sequence cut into many workgroups' pieces
+    (8, 1, 128, 12, 6000, FP8, 16),
+    (16, 2, 64, 8, 4100, FP8, 16),
+    (16, 4, 128, 3, 9000, t.bfloat16, 16),
+    (16, 2, 64, 8, 4100, t.bfloat16, 16),
+    (16, 4, 128, 40, 3000, FP8, 64),     # pages of 4 tiles
+    (8, 2, 128, 24, 5000, t.bfloat16, 32),
 ])
-def test_replicated_heads(hq, hkv, d, batch, long_len, cache_dtype):
+def test_replicated_heads(hq, hkv, d, batch, long_len, cache_dtype, block_size):
     """Fewer than 8 KV heads (dividing 8) run 8 waves per workgroup, 8 / Hkv replicas
     of each head that merge their softmax states at the end of every segment, when
     the merge buffer fits in LDS beside the batch-sized tables and the batch's tile
@@ -556,9 +558,9 @@ def test_replicated_heads(hq, hkv, d, batch, long_len, cache_dtype):
     lengths = [(i * 53) % 97 + 1 for i in range(batch)]
     if long_len:
         lengths[1] = long_len
-    spec = workloads.WorkloadSpec("replicas", batch, hq, hkv, d, lengths, seed=23)
+    spec = workloads.WorkloadSpec("replicas", batch, hq, hkv, d, lengths, seed=23, block_size=block_size)
     w = workloads.build(spec, "cuda")
-    cache = PagedKVCache(w.num_blocks, 16, hkv, d, "cuda", cache_dtype)
+    cache = PagedKVCache(w.num_blocks, block_size, hkv, d, "cuda", cache_dtype)
     workloads.fill_cache(w, cache, "cuda")
     k, v = workloads.new_kv(w, "cuda")
     cache.append_kv(w.new_blocks, w.new_offsets, k, v)
