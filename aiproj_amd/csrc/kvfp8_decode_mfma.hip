@@ -64,10 +64,11 @@ typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 constexpr int kMaxWaves = 8;            // KV heads served by one workgroup at a time
 constexpr int kMaxThreads = 64 * kMaxWaves;
 constexpr int kMinTilesPerGroup = 2;    // a group gets at least 32 tokens per head
-// Waves per CU the grid is sized for (caps the grid): with fewer KV heads than 8 the
-// workgroups are narrower, and fewer, longer ones (one 4-wave group per CU at 4 KV heads)
-// measured faster than filling each CU: 16q/4kv over 64 x 1040 tokens 19.9 -> 19.0 us,
-// 16q/2kv over 32 x 4096 21.7 -> 20.7 us (same-box A/B); 8 KV heads are unaffected.
+// Waves per CU the grid is sized for (caps the grid and sizes the workspace): with fewer
+// KV heads than 8 and no replicas the workgroups are narrower, and fewer, longer ones (one
+// 4-wave group per CU at 4 KV heads) measured faster than filling each CU: 16q/4kv over
+// 64 x 1040 tokens 19.9 -> 19.0 us, 16q/2kv over 32 x 4096 21.7 -> 20.7 us (same-box A/B);
+// 8 KV heads are unaffected.
 constexpr int kWavesPerCu = 4;
 constexpr int kMfmaMaxBatch = 8191;     // LDS: tile prefix (batch + 1) and sequence metadata (batch) int32
 
