@@ -5,7 +5,7 @@ The no-allocation call keeps its workspace in the library's static per-device ar
 Its output must equal the allocating call's bit for bit. Checked here:
   * two calls in a row, the second on a smaller batch (the array keeps the first
     call's contents, and the second must not read them);
-  * MFMA and generic kernels;
+  * MFMA (one wave per KV head, and replicated heads) and generic kernels;
   * a shape whose workspace exceeds the array, refused on the host with KVFP8_ELIMIT
     before anything is launched.
 """
@@ -56,6 +56,19 @@ def test_noalloc_equals_allocating_decode_on_two_calls(first, second):
     """Second call smaller than the first: fewer sequences, fewer partial states."""
     for name in (first, second):
         spec = workloads.spec(name)
+        w, cache = _cache_for(spec)
+        want, got = _decode_both(w.q, cache, workloads.make_context(w))
+        assert t.equal(got, want), name
+
+
+@pytest.mark.gpu
+@t.inference_mode()
+def test_noalloc_with_replicated_heads():
+    """16q/4kv shapes that run 8-wave workgroups with two replicas per KV head (their
+    states merged in LDS), twice in a row, the second smaller."""
+    for name, batch, length in (("rep_a", 64, 1040), ("rep_b", 8, 3000)):
+        spec = workloads.WorkloadSpec(name, batch, 16, 4, 128, [length - 7 * (i % 3) for i in range(batch)],
+                                      seed=52)
         w, cache = _cache_for(spec)
         want, got = _decode_both(w.q, cache, workloads.make_context(w))
         assert t.equal(got, want), name
