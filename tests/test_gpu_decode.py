@@ -404,17 +404,20 @@ def test_decode_split_invariance():
 
 
 @t.inference_mode(False)
-def test_graph_capture_replays_match_eager():
+@pytest.mark.parametrize("hq,hkv,lengths", [
+    (32, 8, [2500, 40, 900, 1, 333]),
+    (16, 4, [2500, 40, 900, 1, 333, 4000, 3500, 120]),     # replicated heads
+])
+def test_graph_capture_replays_match_eager(hq, hkv, lengths):
     # The decode step (append + decode + combine) captured once in a HIP graph and
     # replayed several times, with eager work and synchronizations in between,
     # gives the eager bits on every replay.
-    lengths = [2500, 40, 900, 1, 333]
-    cache = PagedKVCache(sum(-(-n // 16) for n in lengths) + 8, 16, 8, 128, "cuda", FP8)
-    manager, context, _, _ = fill_decode_batch([cache], lengths, 8, 128, 16, t.bfloat16, seed=13)
-    q = t.randn(len(lengths), 32, 128, device="cuda", dtype=t.bfloat16)
+    cache = PagedKVCache(sum(-(-n // 16) for n in lengths) + 8, 16, hkv, 128, "cuda", FP8)
+    manager, context, _, _ = fill_decode_batch([cache], lengths, hkv, 128, 16, t.bfloat16, seed=13)
+    q = t.randn(len(lengths), hq, 128, device="cuda", dtype=t.bfloat16)
     blocks = context.physical_blocks[:len(lengths)].clone()
     offsets = context.block_offsets[:len(lengths)].clone()
-    new_k = t.randn(len(lengths), 8, 128, device="cuda", dtype=t.bfloat16)
+    new_k = t.randn(len(lengths), hkv, 128, device="cuda", dtype=t.bfloat16)
     new_v = t.randn_like(new_k)
 
     def step():
