@@ -545,6 +545,7 @@ def test_large_batch_with_sixteen_kv_heads():
     (16, 2, 64, 8, 4100, t.bfloat16, 16),
     (16, 4, 128, 40, 3000, FP8, 64),     # pages of 4 tiles
     (8, 2, 128, 24, 5000, t.bfloat16, 32),
+    (16, 4, 128, 3, 9000, t.float16, 16),    # f16 cache read with f16 q (f16 products)
 ])
 def test_replicated_heads(hq, hkv, d, batch, long_len, cache_dtype, block_size):
     """Fewer than 8 KV heads (dividing 8) run 8 waves per workgroup, 8 / Hkv replicas
@@ -568,16 +569,17 @@ def test_replicated_heads(hq, hkv, d, batch, long_len, cache_dtype, block_size):
     k, v = workloads.new_kv(w, "cuda")
     cache.append_kv(w.new_blocks, w.new_offsets, k, v)
     ctx = workloads.make_context(w)
-    out = decode_attention_wrapper(w.q, cache, ctx)
-    ref = torch_paged_decode(w.q, cache, w.cache_slots, ctx.context_lengths, w.block_table)
+    q = w.q.to(t.float16) if cache_dtype == t.float16 else w.q
+    out = decode_attention_wrapper(q, cache, ctx)
+    ref = torch_paged_decode(q, cache, w.cache_slots, ctx.context_lengths, w.block_table)
     t.testing.assert_close(out.float(), ref, rtol=NORTH_STAR_RTOL, atol=NORTH_STAR_ATOL)
-    call = prepare_decode(w.q, cache, ctx)
+    call = prepare_decode(q, cache, ctx)
     call.output.fill_(float("nan"))
     call.split()
     call.reduce()
     assert t.equal(call.output.view(t.int16), out.view(t.int16))
     rows = sorted({0, 1, batch - 1})
-    expected = oracle_decode(w.q, cache, w.block_table, w.cache_slots, lengths, rows=rows)
+    expected = oracle_decode(q, cache, w.block_table, w.cache_slots, lengths, rows=rows)
     t.testing.assert_close(out[rows].double().cpu(), t.from_numpy(expected), rtol=NORTH_STAR_RTOL,
                            atol=NORTH_STAR_ATOL)
 
