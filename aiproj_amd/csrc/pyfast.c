@@ -9,6 +9,10 @@
  * pointers (Tensor.data_ptr(), None for a null pointer), sizes, strides and dtype
  * codes, and a float for the softmax scale. Each wrapper returns the C return code.
  *
+ * Like ctypes, each wrapper releases the GIL around the C call: a call can block (the
+ * first call on a device queries device attributes and symbol addresses, and a launch
+ * waits when the stream's queue is full), and other Python threads keep running then.
+ *
  * Built by aiproj_amd/build.py with the host C compiler against the Python headers,
  * linked to libkvfp8.so in the same directory.
  */
@@ -60,7 +64,11 @@ static int parse(PyObject* const* args, Py_ssize_t nargs, Py_ssize_t n, Py_ssize
         int64_t iv[DECODE_N];                                                                \
         float scale = 0.0f;                                                                  \
         if (!parse(args, nargs, DECODE_N, 22, iv, &scale, #fn)) return NULL;                 \
-        return PyLong_FromLong(fn(DECODE_ARGS));                                             \
+        int rc;                                                                              \
+        Py_BEGIN_ALLOW_THREADS                                                               \
+        rc = fn(DECODE_ARGS);                                                                \
+        Py_END_ALLOW_THREADS                                                                 \
+        return PyLong_FromLong(rc);                                                          \
     }
 
 DECODE_WRAPPER(kvfp8_paged_decode)
@@ -73,8 +81,11 @@ static PyObject* py_kvfp8_append_paged_decode(PyObject* self, PyObject* const* a
     int64_t iv[DECODE_N + 11];
     float scale = 0.0f;
     if (!parse(args, nargs, DECODE_N + 11, 22, iv, &scale, "kvfp8_append_paged_decode")) return NULL;
-    const int rc = kvfp8_append_paged_decode(DECODE_ARGS, PTR(27), PTR(28), (int)iv[29], iv[30], iv[31], iv[32],
-                                             iv[33], PTR(34), (int)iv[35], PTR(36), (int)iv[37]);
+    int rc;
+    Py_BEGIN_ALLOW_THREADS
+    rc = kvfp8_append_paged_decode(DECODE_ARGS, PTR(27), PTR(28), (int)iv[29], iv[30], iv[31], iv[32], iv[33],
+                                   PTR(34), (int)iv[35], PTR(36), (int)iv[37]);
+    Py_END_ALLOW_THREADS
     return PyLong_FromLong(rc);
 }
 
@@ -83,10 +94,12 @@ static PyObject* py_kvfp8_quantize_append(PyObject* self, PyObject* const* args,
     (void)self;
     int64_t iv[21];
     if (!parse(args, nargs, 21, -1, iv, NULL, "kvfp8_quantize_append")) return NULL;
-    const int rc = kvfp8_quantize_append(PTR(0), PTR(1), (int)iv[2], iv[3], iv[4], iv[5], iv[6], PTR(7), (int)iv[8],
-                                         PTR(9), (int)iv[10], iv[11], (int32_t)iv[12], (int32_t)iv[13], iv[14],
-                                         (int32_t)iv[15], PTR(16), PTR(17), (float*)PTR(18), (float*)PTR(19),
-                                         PTR(20));
+    int rc;
+    Py_BEGIN_ALLOW_THREADS
+    rc = kvfp8_quantize_append(PTR(0), PTR(1), (int)iv[2], iv[3], iv[4], iv[5], iv[6], PTR(7), (int)iv[8], PTR(9),
+                               (int)iv[10], iv[11], (int32_t)iv[12], (int32_t)iv[13], iv[14], (int32_t)iv[15],
+                               PTR(16), PTR(17), (float*)PTR(18), (float*)PTR(19), PTR(20));
+    Py_END_ALLOW_THREADS
     return PyLong_FromLong(rc);
 }
 
@@ -95,9 +108,12 @@ static PyObject* py_kvfp8_store_append(PyObject* self, PyObject* const* args, Py
     (void)self;
     int64_t iv[20];
     if (!parse(args, nargs, 20, -1, iv, NULL, "kvfp8_store_append")) return NULL;
-    const int rc = kvfp8_store_append(PTR(0), PTR(1), (int)iv[2], iv[3], iv[4], iv[5], iv[6], PTR(7), (int)iv[8],
-                                      PTR(9), (int)iv[10], iv[11], (int32_t)iv[12], (int32_t)iv[13], iv[14],
-                                      (int32_t)iv[15], PTR(16), PTR(17), (int)iv[18], PTR(19));
+    int rc;
+    Py_BEGIN_ALLOW_THREADS
+    rc = kvfp8_store_append(PTR(0), PTR(1), (int)iv[2], iv[3], iv[4], iv[5], iv[6], PTR(7), (int)iv[8], PTR(9),
+                            (int)iv[10], iv[11], (int32_t)iv[12], (int32_t)iv[13], iv[14], (int32_t)iv[15], PTR(16),
+                            PTR(17), (int)iv[18], PTR(19));
+    Py_END_ALLOW_THREADS
     return PyLong_FromLong(rc);
 }
 
