@@ -47,7 +47,7 @@ SIGNATURES = {
     "kvfp8_paged_decode_split": (_INT, _DECODE_ARGS),
     "kvfp8_paged_decode_reduce": (_INT, _DECODE_ARGS),
     "kvfp8_paged_decode_noalloc": (_INT, _DECODE_ARGS[:-3] + [_P]),
-    "kvfp8_append_paged_decode": (_INT, _DECODE_ARGS + [_P, _P, _INT, _I64, _I64, _I64, _I64, _P, _INT, _P, _INT]),
+    "kvfp8_append_paged_decode": (_INT, _DECODE_ARGS + [_P, _P, _INT, _I64, _I64, _I64, _I64, _P, _INT, _P, _INT, _P]),
     "kvfp8_append_decode_supported": (_INT, [_I32, _I32, _I32, _I32, _I64, _I64, _I32, _INT]),
     "kvfp8_rmsnorm_forward": (_INT, [_P, _INT, _I64, _I64, _I32, _P, _INT, ctypes.c_float, _P, _I64, _P, _P]),
     "kvfp8_add_rmsnorm_forward": (_INT, [_P, _P, _INT, _I64, _I64, _I64, _I32, _P, _INT, ctypes.c_float,

@@ -767,6 +767,7 @@ struct NewTokens {
     const void* blocks;
     const void* offsets;
     int blocks64, offsets64;
+    int32_t* refused;
 };
 
 struct Plan {
@@ -1042,7 +1043,7 @@ extern "C" int kvfp8_append_decode_supported(int32_t batch, int32_t num_q_heads,
 extern "C" int kvfp8_append_paged_decode(KVFP8_DECODE_PARAMS, const void* k_new, const void* v_new, int new_dtype,
                                          int64_t k_new_stride_b, int64_t k_new_stride_h, int64_t v_new_stride_b,
                                          int64_t v_new_stride_h, const void* new_blocks, int new_blocks_dtype,
-                                         const void* new_offsets, int new_offsets_dtype) {
+                                         const void* new_offsets, int new_offsets_dtype, int32_t* refused) {
     if (new_dtype != KVFP8_F32 && new_dtype != KVFP8_F16 && new_dtype != KVFP8_BF16) return KVFP8_EDTYPE;
     if ((new_blocks_dtype != KVFP8_I32 && new_blocks_dtype != KVFP8_I64) ||
         (new_offsets_dtype != KVFP8_I32 && new_offsets_dtype != KVFP8_I64))
@@ -1052,8 +1053,16 @@ extern "C" int kvfp8_append_paged_decode(KVFP8_DECODE_PARAMS, const void* k_new,
     if (k_new_stride_h != head_dim || v_new_stride_h != head_dim || k_new_stride_b < 0 || v_new_stride_b < 0 ||
         k_new_stride_b > INT32_MAX || v_new_stride_b > INT32_MAX)
         return KVFP8_ESTRIDE;
-    const NewTokens fresh{k_new, v_new, new_dtype, (int32_t)k_new_stride_b, (int32_t)v_new_stride_b,
-                          new_blocks, new_offsets, new_blocks_dtype == KVFP8_I64, new_offsets_dtype == KVFP8_I64};
+    const NewTokens fresh{k_new,
+                          v_new,
+                          new_dtype,
+                          (int32_t)k_new_stride_b,
+                          (int32_t)v_new_stride_b,
+                          new_blocks,
+                          new_offsets,
+                          new_blocks_dtype == KVFP8_I64,
+                          new_offsets_dtype == KVFP8_I64,
+                          refused};
     return paged_decode(KVFP8_DECODE_ARGS, kPhaseSplit | kPhaseReduce, &fresh);
 }
 
@@ -1142,6 +1151,7 @@ int paged_decode(const void* q, int q_dtype, int64_t q_stride_b, int64_t q_strid
     a.new_offsets = fresh ? fresh->offsets : nullptr;
     a.new_blocks64 = fresh ? fresh->blocks64 : 0;
     a.new_offsets64 = fresh ? fresh->offsets64 : 0;
+    a.new_refused = fresh ? fresh->refused : nullptr;
 
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     hipError_t err;

@@ -46,11 +46,12 @@ struct DecodeArgs {
     int32_t kv_dwords;        // generic kernel: a lane's slice of a K/V row is read as whole dwords
     int32_t q_dtype;          // grouped kernel: element type of q and out (kvfp8_dtype)
     int32_t group_heads;      // grouped kernel: q heads per work unit (of one KV head's group)
-    // Fused append (kvfp8_append_paged_decode): the new token of every sequence,
-    // rows [batch, Hkv, D] with element strides (row stride, D, 1), quantized into
-    // the cache at (new_blocks[b], new_offsets[b]), the sequence's last attended
-    // position, before it is attended. Read only by the kernels built for the fused
-    // call.
+    // Fused append (kvfp8_append_paged_decode; new_k is null otherwise): the new
+    // token of every sequence, rows [batch, Hkv, D] with element strides (row
+    // stride, D, 1), quantized into the cache at (new_blocks[b], new_offsets[b])
+    // when that is the sequence's last attended position, before it is attended.
+    // Any other location is refused: no write, 1 stored to *new_refused (when not
+    // null). Read only by the kernels built for the fused call.
     const void* new_k;
     const void* new_v;
     int32_t new_dtype;
@@ -58,6 +59,7 @@ struct DecodeArgs {
     const void* new_blocks;
     const void* new_offsets;
     int32_t new_blocks64, new_offsets64;
+    int32_t* new_refused;
 };
 
 __device__ __forceinline__ int64_t load_i(const void* p, int is64, int64_t i) {
@@ -67,14 +69,23 @@ __device__ __forceinline__ int64_t load_i(const void* p, int is64, int64_t i) {
 // Attended tokens of sequence b: context_lengths[b] clipped to what the block
 // table can address (reference decode_attention.py:293-297 masks logical blocks
 // at or past the table width), and 0 for a slot outside the table.
-__device__ __forceinline__ int64_t seq_tokens(const DecodeArgs& a, int b, int64_t* slot_out) {
+__device__ __forceinline__ int64_t seq_tokens(const DecodeArgs& a, int b, int64_t* slot_out,
+                                              int64_t* raw_out = nullptr) {
     const int64_t slot = load_i(a.slots, a.slots64, b);
-    int64_t len = load_i(a.ctx, a.ctx64, b);
+    const int64_t raw = load_i(a.ctx, a.ctx64, b);
     const int64_t cap = a.bt_width * a.block_size;
-    len = len < 0 ? 0 : (len > cap ? cap : len);
+    int64_t len = raw < 0 ? 0 : (raw > cap ? cap : raw);
     if (slot < 0 || slot >= a.bt_rows) len = 0;
     *slot_out = slot;
+    if (raw_out) *raw_out = raw;
     return len;
+}
+
+// Fused append + decode: whether sequence b's new token, at position
+// context_lengths[b] - 1, is one the decode attends: its slot is a table row and
+// 1 <= context_lengths[b] <= bt_width * block_size. Only such a token is written.
+__device__ __forceinline__ bool new_token_attended(const DecodeArgs& a, int64_t slot, int64_t raw_len) {
+    return slot >= 0 && slot < a.bt_rows && raw_len >= 1 && raw_len <= a.bt_width * a.block_size;
 }
 
 __device__ __forceinline__ int32_t seq_chunks(int64_t len, int32_t chunk_tokens) {

@@ -151,7 +151,10 @@ __device__ __forceinline__ int step_token(int i, int j) {
 // Tile prefix over the batch in LDS: prefix[b] = sum_{i<b} ceil(len_i / 16),
 // and meta[b] = slot_b * 32 + (tokens in the last tile of b) for sequences with
 // tokens (slots are below 2^26, checked by the host). Per-thread runs, a shuffle
-// scan inside each wave, then the wave totals.
+// scan inside each wave, then the wave totals. kMark (fused append + decode): bit
+// 31 of meta[b] marks a sequence whose new token, at position len_b - 1, is one
+// the decode attends (new_token_attended).
+template <bool kMark>
 __device__ void build_tile_prefix(const DecodeArgs& a, int32_t* prefix, int32_t* meta, int32_t* wave_total) {
     const int threads = blockDim.x, tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -161,11 +164,12 @@ __device__ void build_tile_prefix(const DecodeArgs& a, int32_t* prefix, int32_t*
     for (int i = 0; i < per; ++i) {
         const int b = begin + i;
         if (b < a.batch) {
-            int64_t slot;
-            const int64_t len = seq_tokens(a, b, &slot);
+            int64_t slot, raw;
+            const int64_t len = seq_tokens(a, b, &slot, &raw);
             const int32_t tiles = (int32_t)((len + 15) >> 4);
+            const int32_t mark = kMark && new_token_attended(a, slot, raw) ? INT32_MIN : 0;
             prefix[b] = local;
-            meta[b] = tiles > 0 ? (int32_t)(slot << 5) | (int32_t)(len - 16 * (int64_t)(tiles - 1)) : 0;
+            meta[b] = tiles > 0 ? (int32_t)(slot << 5) | (int32_t)(len - 16 * (int64_t)(tiles - 1)) | mark : 0;
             local += tiles;
         }
     }
@@ -597,9 +601,14 @@ __device__ __forceinline__ void compute_step(WaveState<C>& st, const StepData<C,
 // propagates NaN; scale = amax / 448 by IEEE division, 1 when amax is 0 or NaN;
 // codes from the corrected reciprocal on finite rows, else clamp and encode).
 // The row goes where the caller's write location (new_blocks[b], new_offsets[b])
-// points, and nowhere when that lies outside the pool, as in the append kernel.
-// The caller guarantees that this location is the sequence's last attended
-// position, so it lies in the tile this wave reads last.
+// points, and nowhere when that lies outside the pool, as in the append kernel,
+// provided that location is the sequence's last attended position: page
+// block_table[slot, (len - 1) / block_size] (the entry fetch() reads) at offset
+// (len - 1) % block_size, with the new token attended (meta bit 31). It then lies in
+// the tile this wave reads last, and no other wave reads it. Any other location
+// (or a new token the decode does not attend) is refused: nothing is stored, 1 goes
+// to *new_refused, and the wave attends the row the cache holds, as the decode of the
+// unchanged cache would. The write therefore never races with a read.
 // Lane l holds elements C l .. C l + C - 1. fetch() issues the loads and put()
 // quantizes and stores; the wave's own loads of that page row come after put()
 // in its instruction order, which the memory pipeline keeps for one wave, so
@@ -615,6 +624,8 @@ template <int C>
 struct NewRow {
     uint32_t k_lo[C], k_hi[C], v_lo[C], v_hi[C];   // the two 16-bit loads of each element
     uint32_t page_lo, page_hi, off_lo, off_hi;
+    uint32_t last_page;    // block-table entry of the last attended position
+    int32_t last_off;      // its offset in the page, or -1 when the new token is not attended
     int32_t idx64;         // bit 0: new_blocks is int64; bit 1: new_offsets is int64
     int32_t dtype;
     int32_t h;             // KV head
@@ -623,8 +634,11 @@ struct NewRow {
 typedef const __attribute__((address_space(4))) uint32_t* const_u32_ptr;
 typedef const __attribute__((address_space(1))) uint16_t* const_g_u16_ptr;   // global memory
 
+// table_row, len, attended: the sequence's block-table row, its attended length
+// (at least 1) and whether its new token is attended (meta bit 31).
 template <int C>
-__device__ __forceinline__ void fetch_new_token(const MfmaArgs& a, int b, int h, int lane, NewRow<C>& r) {
+__device__ __forceinline__ void fetch_new_token(const MfmaArgs& a, int b, int h, int lane, NewRow<C>& r,
+                                                const int32_t* table_row, int64_t len, bool attended) {
     constexpr int D = 64 * C;
     // The new-row fields are read from the kernel-argument segment here, where they
     // are used: the empty asm keeps the compiler from hoisting these loads to the
@@ -645,6 +659,9 @@ __device__ __forceinline__ void fetch_new_token(const MfmaArgs& a, int b, int h,
     r.page_hi = *(const_u32_ptr)(pb_at + (b64 ? 4 : 0));
     r.off_lo = *(const_u32_ptr)po_at;
     r.off_hi = *(const_u32_ptr)(po_at + (o64 ? 4 : 0));
+    const int32_t bs_shift = na->bs_shift;
+    r.last_page = *(const_u32_ptr)(uintptr_t)(table_row + ((len - 1) >> bs_shift));
+    r.last_off = attended ? (int32_t)((len - 1) & ((1 << bs_shift) - 1)) : -1;
     r.idx64 = (b64 ? 1 : 0) | (o64 ? 2 : 0);
     r.dtype = dtype;
     r.h = h;
@@ -681,6 +698,15 @@ __device__ __forceinline__ void put_new_token(const MfmaArgs& a, const NewRow<C>
     }
     const int64_t page = (r.idx64 & 1) ? (int64_t)(((uint64_t)r.page_hi << 32) | r.page_lo) : (int64_t)(int32_t)r.page_lo;
     const int64_t off = (r.idx64 & 2) ? (int64_t)(((uint64_t)r.off_hi << 32) | r.off_lo) : (int64_t)(int32_t)r.off_lo;
+    if (r.last_off < 0 || page != (int64_t)(int32_t)r.last_page || off != r.last_off) {
+        // The flag's address is read here, where it is used (see fetch_new_token).
+        uint64_t kargs = (uint64_t)(uintptr_t)__builtin_amdgcn_kernarg_segment_ptr();
+        __asm__ volatile("" : "+s"(kargs));
+        typedef const __attribute__((address_space(4))) DecodeArgs* const_args_ptr;
+        int32_t* flag = ((const_args_ptr)(uintptr_t)(kargs + offsetof(MfmaArgs, d)))->new_refused;
+        if (lane == 0 && flag != nullptr) *flag = 1;
+        return;
+    }
     if (page < 0 || page >= a.d.num_blocks || off < 0 || off >= a.d.block_size) return;
     const int64_t row = (page * a.d.block_size + off) * a.d.num_kv_heads + r.h;
     float xk[C], xv[C];
@@ -731,7 +757,7 @@ decode_mfma_kernel(MfmaArgs a) {
     if (threadIdx.x < kMaxWaves) progress[threadIdx.x] = 0;   // visible after the plan's barriers
 
     int32_t* meta = prefix + a.d.batch + 1;
-    build_tile_prefix(a.d, prefix, meta, wave_total);
+    build_tile_prefix<kAppend>(a.d, prefix, meta, wave_total);
     const int32_t total = prefix[a.d.batch];
     const int32_t want = (total + kMinTilesPerGroup - 1) / kMinTilesPerGroup;
     const int32_t groups = min((int32_t)gridDim.x, max(want, 1));
@@ -752,15 +778,11 @@ decode_mfma_kernel(MfmaArgs a) {
     float4* stage = stage_all[wave];
 
     if constexpr (kAppend) {
-        // Sequences with no attended tile are read by no workgroup; their new rows
-        // are still written (workgroup b % groups writes sequence b).
-        for (int b = w; b < a.d.batch; b += groups) {
-            if (uniform(prefix[b + 1]) != uniform(prefix[b])) continue;
-            for (int h = wave; h < a.d.num_kv_heads; h += waves) {
-                NewRow<C> fresh;
-                fetch_new_token<C>(a, uniform(b), h, lane, fresh);
-                put_new_token<C>(a, fresh, lane);
-            }
+        // Sequences with no attended tile (no context, or a slot outside the table)
+        // attend no new token: their rows are refused (workgroup b % groups says so).
+        if (threadIdx.x == 0 && a.d.new_refused != nullptr) {
+            for (int b = w; b < a.d.batch; b += groups)
+                if (prefix[b + 1] == prefix[b]) *a.d.new_refused = 1;
         }
     }
 
@@ -806,7 +828,7 @@ decode_mfma_kernel(MfmaArgs a) {
             const int slot_index = 2 * w + (start >= seq0 ? 0 : 1);
             // Slot and length from the LDS metadata (the segment has tiles).
             const int32_t mt = uniform(meta[b]);
-            const int64_t slot = mt >> 5;
+            const int64_t slot = (mt >> 5) & ((1 << 26) - 1);
             const int64_t len = 16 * (int64_t)(seq1 - seq0 - 1) + (mt & 31);
             const int32_t* table_row = a.d.block_table + slot * a.d.bt_width;
             // This workgroup attends over the sequence's last tile: it writes the
@@ -817,7 +839,7 @@ decode_mfma_kernel(MfmaArgs a) {
             const bool append = kAppend && seg1 == seq1 && (!kRep || ((t1 - 1 - t0) >> 1) % reps == rep_r);
             NewRow<C> fresh;
             if constexpr (kAppend) {
-                if (append) fetch_new_token<C>(a, b, h, lane, fresh);
+                if (append) fetch_new_token<C>(a, b, h, lane, fresh, table_row, len, mt < 0);
             }
             const int32_t T0 = t0 + 2 * rep_r;     // this wave's first step
             const bool put_early = t1 - 1 < T0 + (ES == 1 ? 2 * dT : 2);

@@ -75,16 +75,16 @@ DECODE_WRAPPER(kvfp8_paged_decode)
 DECODE_WRAPPER(kvfp8_paged_decode_split)
 DECODE_WRAPPER(kvfp8_paged_decode_reduce)
 
-/* kvfp8_append_paged_decode: the decode arguments, then the 11 of the new rows. */
+/* kvfp8_append_paged_decode: the decode arguments, then the 12 of the new rows. */
 static PyObject* py_kvfp8_append_paged_decode(PyObject* self, PyObject* const* args, Py_ssize_t nargs) {
     (void)self;
-    int64_t iv[DECODE_N + 11];
+    int64_t iv[DECODE_N + 12];
     float scale = 0.0f;
-    if (!parse(args, nargs, DECODE_N + 11, 22, iv, &scale, "kvfp8_append_paged_decode")) return NULL;
+    if (!parse(args, nargs, DECODE_N + 12, 22, iv, &scale, "kvfp8_append_paged_decode")) return NULL;
     int rc;
     Py_BEGIN_ALLOW_THREADS
     rc = kvfp8_append_paged_decode(DECODE_ARGS, PTR(27), PTR(28), (int)iv[29], iv[30], iv[31], iv[32], iv[33],
-                                   PTR(34), (int)iv[35], PTR(36), (int)iv[37]);
+                                   PTR(34), (int)iv[35], PTR(36), (int)iv[37], (int32_t*)PTR(38));
     Py_END_ALLOW_THREADS
     return PyLong_FromLong(rc);
 }

@@ -19,8 +19,9 @@ one at a time.
 
 `append_decode_attention(q, ks, vs, paged_kv_cache, cache_batch_context)` is the
 decode step's append and attention together (reference `model/attention.py:86-99`
-makes the two calls back to back). On an FP8 cache the decode kernel itself writes
-each sequence's new token (`kvfp8_append_paged_decode`), so the step has no
+makes the two calls back to back). On an FP8 cache the decode kernel itself
+writes each sequence's new token (`kvfp8_append_paged_decode`), after checking on the
+device that its location is the sequence's last attended position, so the step has no
 separate append launch; other caches and shapes make the two calls.
 """
 
@@ -177,21 +178,25 @@ def _fused_supported(b, hq, hkv, d, bt_rows, bt_width, block_size, kv_code) -> b
     return _native.lib().kvfp8_append_decode_supported(b, hq, hkv, d, bt_rows, bt_width, block_size, kv_code) == 1
 
 
-def append_decode_attention(q, ks, vs, paged_kv_cache, cache_batch_context):
+def append_decode_attention(q, ks, vs, paged_kv_cache, cache_batch_context, refused=None):
     """`paged_kv_cache.append_kv(ctx.physical_blocks, ctx.block_offsets, ks, vs)` followed by
     `decode_attention_wrapper(q, paged_kv_cache, ctx)`, the decode step of reference
-    `model/attention.py:86-99`, with the same results (cache codes and scales bit-identical).
+    `model/attention.py:86-99`, with the same results (cache codes, scales and output
+    bit-identical).
 
     ks, vs: [B, Hkv, D], the new token of every sequence of the batch.
 
-    The write happens inside the decode kernel (one call, no separate append launch)
-    when the container says its write locations are the sequences' last attended
-    positions (`appends_last_position`: set by `PageAllocator.create_container` after
-    validating a one-token-per-sequence batch at the committed lengths, and by the
-    runtime's decode step, which builds such metadata) and the cache is e4m3fn with a
-    shape the MFMA kernel handles. The kernel writes row b at
-    (physical_blocks[b], block_offsets[b]), so the cache holds what the two calls would
-    write. Every other case makes the two calls.
+    The step is one fused call (`kvfp8_append_paged_decode`) when the container says
+    its write locations are the sequences' last attended positions
+    (`appends_last_position`: set by `PageAllocator.create_container` after validating a
+    one-token-per-sequence batch at the committed lengths, and by the runtime's decode
+    step, which builds such metadata) and the cache is e4m3fn with a shape the MFMA
+    kernel handles. The decode kernel writes row b at (physical_blocks[b],
+    block_offsets[b]) before it reads that position. It checks every location against
+    the block table on the device: a sequence whose location is not its last attended
+    position has its row refused (not written; its output attends the cache as it is)
+    and 1 is stored into `refused` (an int32 device tensor of one element that the
+    caller zeroes, or None). Every other case makes the two calls.
     """
     cache, ctx = paged_kv_cache, cache_batch_context
     b, hq, d = q.shape
@@ -199,6 +204,8 @@ def append_decode_attention(q, ks, vs, paged_kv_cache, cache_batch_context):
     expected = (b, hkv, d)
     if ks.shape != expected or vs.shape != expected:
         raise ValueError(f"append_decode_attention: new K/V must be {expected}")
+    if refused is not None and (refused.dtype != t.int32 or refused.numel() != 1):
+        raise ValueError("append_decode_attention: refused must be one int32 element")
     blocks, offsets = ctx.physical_blocks, ctx.block_offsets
     fused = (getattr(ctx, "appends_last_position", False)
              and cache.quantized and ks.dtype in _Q_DTYPES and vs.dtype in _Q_DTYPES
@@ -208,7 +215,7 @@ def append_decode_attention(q, ks, vs, paged_kv_cache, cache_batch_context):
     if not fused:
         cache.append_kv(blocks, offsets, ks, vs)
         return decode_attention_wrapper(q, cache, ctx)
-    _native.require_gpu(ks, vs, cache.k, blocks, offsets, what="append_decode_attention")
+    _native.require_gpu(ks, vs, cache.k, blocks, offsets, refused, what="append_decode_attention")
     call = prepare_decode(q, cache, ctx)
     if call.args is None:
         return call.output
@@ -224,6 +231,7 @@ def append_decode_attention(q, ks, vs, paged_kv_cache, cache_batch_context):
     rc = _native.fn("kvfp8_append_paged_decode")(
         *call.args, ks.data_ptr(), vs.data_ptr(), _native.dtype_code(ks.dtype),
         ks.stride(0), ks.stride(1), vs.stride(0), vs.stride(1),
-        blocks.data_ptr(), _native.dtype_code(blocks.dtype), offsets.data_ptr(), _native.dtype_code(offsets.dtype))
+        blocks.data_ptr(), _native.dtype_code(blocks.dtype), offsets.data_ptr(), _native.dtype_code(offsets.dtype),
+        _native.ptr(refused))
     _native.check(rc, "kvfp8_append_paged_decode")
     return call.output

@@ -241,21 +241,28 @@ int kvfp8_prefill_attention(const void* q_dev, const void* k_dev, const void* v_
  *
  * Replaces the two calls the reference makes back to back in its decode step,
  * reference src/torch_llm/model/attention.py:86-99 (PagedKVCache.append_kv, then
- * decode_attention_wrapper). Row b of k_new/v_new is written at
- * (new_blocks[b], new_offsets[b]) with the kvfp8_quantize_append rule (codes and
- * scales bit-identical to it; locations outside the pool are skipped), before the
- * attention reads it. The caller guarantees that this location is sequence b's last
- * attended position, page block_table[slots[b], (context_lengths[b] - 1) /
- * block_size] at offset (context_lengths[b] - 1) % block_size: the write is ordered
- * before the reads of that position only. With that guarantee the results equal the
- * two calls bit for bit.
+ * decode_attention_wrapper). The new token of sequence b is its last attended
+ * position L - 1 (L = context_lengths[b]), page block_table[slots[b], (L - 1) /
+ * block_size] at offset (L - 1) % block_size. The wave that serves KV head h over
+ * the sequence's last tile quantizes head h of row b of k_new/v_new with the
+ * kvfp8_quantize_append rule and stores it at (new_blocks[b], new_offsets[b])
+ * before it reads that tile; no other wave reads that row. Results (cache codes and
+ * scales, and outputs) equal the two calls bit for bit.
  *
- * Takes the kvfp8_paged_decode arguments, then the new rows: k_new/v_new
- * [batch, H_kv, D] (f32/f16/bf16, one dtype) with element strides (stride_b,
- * stride_h, 1), stride_h == D and stride_b below 2^31, then the write locations
- * new_blocks/new_offsets [batch] (int32/int64). e4m3fn caches on the MFMA kernel
- * only: other shapes return KVFP8_ESHAPE before launching anything
- * (kvfp8_append_decode_supported says which).
+ * The kernel checks every write location on the device against the block table.
+ * A location that is not the sequence's last attended position, or a sequence that
+ * attends no new token (L = 0, L beyond the table, a slot outside it), is refused:
+ * nothing is stored for it, 1 is stored to *refused_dev (when not NULL; the call
+ * never clears it, so the caller zeroes it before), and its output is that of
+ * kvfp8_paged_decode on the cache as it is. So the write never races with a read.
+ * A matching location outside the pool is skipped, as in kvfp8_quantize_append.
+ *
+ * Takes the kvfp8_paged_decode arguments (the same workspace size), then the new
+ * rows: k_new/v_new [batch, H_kv, D] (f32/f16/bf16, one dtype) with element strides
+ * (stride_b, stride_h, 1), stride_h == D and stride_b below 2^31, then the write locations
+ * new_blocks/new_offsets [batch] (int32/int64), then refused_dev (int32, may be
+ * NULL). e4m3fn caches on the MFMA kernel only: other shapes return KVFP8_ESHAPE
+ * before launching anything (kvfp8_append_decode_supported says which).
  */
 int kvfp8_append_paged_decode(const void* q_dev, int q_dtype, int64_t q_stride_b, int64_t q_stride_h,
                               int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
@@ -271,7 +278,8 @@ int kvfp8_append_paged_decode(const void* q_dev, int q_dtype, int64_t q_stride_b
                               int64_t k_new_stride_b, int64_t k_new_stride_h,
                               int64_t v_new_stride_b, int64_t v_new_stride_h,
                               const void* new_blocks_dev, int new_blocks_dtype,
-                              const void* new_offsets_dev, int new_offsets_dtype);
+                              const void* new_offsets_dev, int new_offsets_dtype,
+                              int32_t* refused_dev);
 
 /* 1 when kvfp8_append_paged_decode handles these shapes (e4m3fn cache on the MFMA
  * kernel), else 0. Shapes only; pointer alignment is checked by the call. */

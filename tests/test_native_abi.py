@@ -224,17 +224,21 @@ def test_fused_append_and_swiglu_argument_checks(lib):
     decode = [fake, _native.BF16, 0, 0, 4, 8, 2, 128, fake, fake, _native.E4M3FN, fake, fake,
               64, 16, fake, 4, 64, fake, _native.I64, fake, _native.I32, 0.125, fake, fake, 1 << 30, None]
     fused = lib.kvfp8_append_paged_decode
-    where = (fake, _native.I64, fake, _native.I32)                                 # write locations
+    where = (fake, _native.I64, fake, _native.I32, None)                   # write locations, no refusal flag
     assert fused(*decode, fake, fake, _native.E4M3FN, 256, 128, 256, 128, *where) == -1    # new-row dtype
     assert fused(*decode, fake, fake, _native.BF16, 256, 128, 256, 128,
-                 fake, _native.F32, fake, _native.I32) == -1                               # location dtype
+                 fake, _native.F32, fake, _native.I32, fake) == -1                         # location dtype
     assert fused(*decode, None, fake, _native.BF16, 256, 128, 256, 128, *where) == -4      # no new rows
     assert fused(*decode, fake, fake, _native.BF16, 256, 128, 256, 128,
-                 None, _native.I64, fake, _native.I32) == -4                               # no locations
+                 None, _native.I64, fake, _native.I32, None) == -4                         # no locations
     assert fused(*decode, fake, fake, _native.BF16, 256, 64, 256, 128, *where) == -3       # heads not contiguous
     bf16_cache = list(decode)
     bf16_cache[10] = _native.BF16
     assert fused(*bf16_cache, fake, fake, _native.BF16, 256, 128, 256, 128, *where) == -2  # not on the fused kernel
+    # An empty batch passes every check and launches nothing; rows need element alignment only.
+    empty = list(decode)
+    empty[4] = 0
+    assert fused(*empty, ctypes.c_void_p(18), fake, _native.BF16, 257, 128, 255, 128, *where) == 0
 
     silu = lib.kvfp8_silu_mul
     assert silu(fake, _native.E4M3FN, 4, 8, 16, fake, 8, None) == -1
@@ -263,10 +267,10 @@ def test_fast_bindings_match_ctypes_on_host_checks(lib):
         with pytest.raises(TypeError):
             getattr(fast, name)(*decode[:-1])
         assert _native.fn(name) is getattr(fast, name)
-    where = [fake, _native.I64, fake, _native.I32]
+    where = [fake, _native.I64, fake, _native.I32, fake]
     fused_cases = [
         decode + [fake, fake, _native.E4M3FN, 256, 128, 256, 128] + where,
-        decode + [fake, fake, _native.BF16, 256, 128, 256, 128, fake, _native.F32, fake, _native.I32],
+        decode + [fake, fake, _native.BF16, 256, 128, 256, 128, fake, _native.F32, fake, _native.I32, None],
         decode + [None, fake, _native.BF16, 256, 128, 256, 128] + where,
         decode + [fake, fake, _native.BF16, 256, 64, 256, 128] + where,
     ]
