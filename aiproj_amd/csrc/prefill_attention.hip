@@ -939,6 +939,115 @@ int fa_device_cus() {
     return cus[dev];
 }
 
+// ---------------------------------------------------------------------------
+// Vector-ALU kernel for the head sizes the matrix-core kernels do not take (not a
+// multiple of 8, or above 128; up to kGenMaxD), as the reference's Triton kernel
+// takes any head size (reference kernals/flash_attention.py:72 pads it to a power
+// of two). One wave per (sequence, q head, query row): the row's q is staged in the
+// wave's LDS slot as float32; each lane scores one key of a 64-key block (a float32
+// dot product over D), the block enters the online softmax (base 2), and each lane
+// accumulates D / 64 output dims (rounded up: ND per lane) from the block's V rows,
+// the probabilities broadcast from their lanes. Element loads only: no alignment
+// beyond the element's. Rows past max_seq_len are not computed.
+constexpr int kGenMaxD = 512;
+constexpr int kGenWaves = 4;
+
+template <int IT, int ND>
+__global__ void __launch_bounds__(64 * kGenWaves)
+prefill_generic_kernel(PrefillArgs a) {
+    using T = typename Elem<IT>::T;
+    __shared__ float q_lds[kGenWaves][kGenMaxD];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    // Unit (sequence b, q head hq, row r): consecutive rows of one head share a workgroup.
+    const int64_t unit = (int64_t)blockIdx.x * kGenWaves + wave;
+    const int64_t per_b = (int64_t)a.hq * a.max_len;
+    const int b = (int)(unit / per_b);
+    if (b >= a.batch) return;
+    const int64_t rest = unit - (int64_t)b * per_b;
+    const int hq = (int)(rest / a.max_len);
+    const int r = (int)(rest - (int64_t)hq * a.max_len);
+    int64_t s0, s1;
+    if (a.cu64) {
+        s0 = reinterpret_cast<const int64_t*>(a.cu)[b];
+        s1 = reinterpret_cast<const int64_t*>(a.cu)[b + 1];
+    } else {
+        s0 = reinterpret_cast<const int32_t*>(a.cu)[b];
+        s1 = reinterpret_cast<const int32_t*>(a.cu)[b + 1];
+    }
+    s0 = s0 < 0 ? 0 : s0;
+    s1 = s1 > a.total_tokens ? a.total_tokens : s1;
+    const int64_t len = s1 > s0 ? s1 - s0 : 0;
+    if (r >= len) return;                  // r < max_seq_len by construction
+
+    const int D = a.d;
+    const int hk = hq / (a.hq / a.hkv);
+    const int64_t tok = s0 + r;
+    const int64_t kv_stride = (int64_t)a.hkv * D;
+    const T* qrow = reinterpret_cast<const T*>(a.q) + (tok * a.hq + hq) * D;
+    const T* kbase = reinterpret_cast<const T*>(a.k) + s0 * kv_stride + (int64_t)hk * D;
+    const T* vbase = reinterpret_cast<const T*>(a.v) + s0 * kv_stride + (int64_t)hk * D;
+    float* qs = q_lds[wave];
+    for (int d = lane; d < D; d += 64) qs[d] = Elem<IT>::load(qrow[d]);
+    __builtin_amdgcn_wave_barrier();      // one wave's LDS operations complete in order
+
+    float m = kNegInf, l = 0.0f;
+    float acc[ND];
+#pragma unroll
+    for (int e = 0; e < ND; ++e) acc[e] = 0.0f;
+    for (int k0 = 0; k0 <= r; k0 += 64) {
+        const int key = k0 + lane;
+        const bool valid = key <= r;     // causal, and r < len
+        float s = kNegInf;
+        if (valid) {
+            const T* krow = kbase + key * kv_stride;
+            float dot = 0.0f;
+            for (int d = 0; d < D; ++d) dot += qs[d] * Elem<IT>::load(krow[d]);
+            s = dot * a.scale_log2;
+        }
+        float mb = s;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) mb = fmaxf(mb, __shfl_xor(mb, o));
+        const float m_new = fmaxf(m, mb);              // finite: key k0 <= r is valid
+        const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+        const float p = valid ? __builtin_amdgcn_exp2f(s - m_new) : 0.0f;
+        float ps = p;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) ps += __shfl_xor(ps, o);
+        l = l * alpha + ps;
+#pragma unroll
+        for (int e = 0; e < ND; ++e) acc[e] *= alpha;
+        const int nkeys = min(64, r - k0 + 1);
+        for (int jj = 0; jj < nkeys; ++jj) {
+            const float pj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), jj));
+            const T* vrow = vbase + (int64_t)(k0 + jj) * kv_stride;
+#pragma unroll
+            for (int e = 0; e < ND; ++e) {
+                const int d = lane + 64 * e;
+                if (d < D) acc[e] += pj * Elem<IT>::load(vrow[d]);
+            }
+        }
+        m = m_new;
+    }
+    T* orow = reinterpret_cast<T*>(a.out) + (tok * a.hq + hq) * D;
+    const float inv = 1.0f / l;                      // l >= 1: the row's largest score enters as 1
+#pragma unroll
+    for (int e = 0; e < ND; ++e) {
+        const int d = lane + 64 * e;
+        if (d < D) orow[d] = Elem<IT>::store(acc[e] * inv);
+    }
+    if (lane == 0) a.lse[tok * a.hq + hq] = (m + __builtin_log2f(l)) * kLn2;
+}
+
+template <int IT>
+hipError_t launch_generic_prefill(const PrefillArgs& a, int64_t blocks, hipStream_t s) {
+    const dim3 grid((unsigned)blocks), block(64 * kGenWaves);
+    if (a.d <= 64) hipLaunchKernelGGL((prefill_generic_kernel<IT, 1>), grid, block, 0, s, a);
+    else if (a.d <= 128) hipLaunchKernelGGL((prefill_generic_kernel<IT, 2>), grid, block, 0, s, a);
+    else if (a.d <= 256) hipLaunchKernelGGL((prefill_generic_kernel<IT, 4>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((prefill_generic_kernel<IT, 8>), grid, block, 0, s, a);
+    return hipGetLastError();
+}
+
 template <int IT>
 hipError_t launch_prefill(const PrefillArgs& a, int64_t blocks, hipStream_t s) {
     if (a.d <= 64)
@@ -963,11 +1072,14 @@ extern "C" int kvfp8_prefill_attention(const void* q, const void* k, const void*
     if (total_tokens < 0 || batch < 0 || max_seq_len < 0 || num_q_heads <= 0 || num_kv_heads <= 0 ||
         num_q_heads % num_kv_heads != 0)
         return KVFP8_ESHAPE;
-    // Head sizes: multiples of 8 up to 128 (8-element operand runs).
-    if (head_dim <= 0 || head_dim % 8 != 0 || head_dim > 128) return KVFP8_ESHAPE;
+    // Head sizes: multiples of 8 up to 128 on the matrix cores (8-element operand
+    // runs), every other size up to kGenMaxD on the vector-ALU kernel.
+    if (head_dim <= 0 || head_dim > kGenMaxD) return KVFP8_ESHAPE;
+    const bool matrix = head_dim % 8 == 0 && head_dim <= 128;
     if (total_tokens == 0 || batch == 0 || max_seq_len == 0) return KVFP8_OK;
     if (!q || !k || !v || !out || !lse || !cu_seqlens) return KVFP8_ENULL;
-    if ((((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out) & 15) != 0) return KVFP8_ESTRIDE;
+    const uintptr_t align = matrix ? 15 : (dtype == KVFP8_F32 ? 3 : 1);
+    if ((((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out) & align) != 0) return KVFP8_ESTRIDE;
     PrefillArgs a;
     a.q = reinterpret_cast<const uint8_t*>(q);
     a.k = reinterpret_cast<const uint8_t*>(k);
@@ -987,6 +1099,16 @@ extern "C" int kvfp8_prefill_attention(const void* q, const void* k, const void*
     a.total_tokens = total_tokens;
     a.scale_log2 = scale * 1.44269504088896340736f;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (!matrix) {
+        const int64_t units = (int64_t)batch * num_q_heads * max_seq_len;
+        const int64_t blocks = (units + kGenWaves - 1) / kGenWaves;
+        if (blocks >= ((int64_t)1 << 31)) return KVFP8_ELIMIT;
+        switch (dtype) {
+            case KVFP8_F32: return (int)launch_generic_prefill<KVFP8_F32>(a, blocks, s);
+            case KVFP8_F16: return (int)launch_generic_prefill<KVFP8_F16>(a, blocks, s);
+            default: return (int)launch_generic_prefill<KVFP8_BF16>(a, blocks, s);
+        }
+    }
     // 16-bit inputs with D 64 or 128: the wide-tile kernel, whose item and token
     // indices are int32 (larger inputs take the general kernel below).
     const int fa_rows = kFaRows * kFaWaves / a.heads_per_block;

@@ -18,8 +18,9 @@ The backward (`flash_attention_backward`, reference `:213-...`) is training-side
 part of the prefill path: it is written with PyTorch float32 operations on the device
 from the saved `lse`, sequence by sequence (it reads the sequence bounds on the host).
 
-Head sizes are multiples of 8 up to 128 (`ValueError` otherwise); the reference pads
-any size to a power of two.
+Head sizes 1 to 512 (`ValueError` otherwise), like the reference, which pads any size
+to a power of two (`:72`): multiples of 8 up to 128 run on the matrix-core kernels, every
+other size on a vector-ALU kernel.
 """
 
 from __future__ import annotations

@@ -225,7 +225,9 @@ int kvfp8_add_rmsnorm_forward(const void* x_dev, const void* update_dev, int dty
  *   out [T, Hq, D] (q's dtype) and lse [T, Hq] float32 = m + log(sum exp(s - m)) of
  *   the scaled scores s = scale * q.k. Rows outside every sequence are not written;
  *   only the first max_seq_len rows of each sequence are computed.
- *   head_dim: multiple of 8, at most 128. Pointers 16-byte aligned.
+ *   head_dim 1..512: multiples of 8 up to 128 run on the matrix cores (pointers
+ *   16-byte aligned), every other size on a vector-ALU kernel (pointers aligned to
+ *   the element size).
  * Replaces the forward of reference src/torch_llm/kernals/flash_attention.py:51-211
  * (flash_attention_forward and flash_attention_forward_kernal).
  */

@@ -169,10 +169,27 @@ def test_config5_prefill_shape_against_float32_torch():
 
 
 @t.inference_mode()
+@pytest.mark.parametrize("dtype", [t.float32, t.bfloat16])
+@pytest.mark.parametrize("head_dim", [12, 20, 24, 96, 136, 192, 256, 300])
+def test_prefill_head_sizes_the_reference_takes(dtype, head_dim):
+    """Head sizes beyond the matrix-core kernels' (not a multiple of 8, or above 128)
+    run on the vector-ALU kernel; 24 and 96 stay on the matrix cores. Against the
+    float64 oracle over ragged lengths, with lse (reference kernals/flash_attention.py:72
+    takes any head size)."""
+    q, k, v, cu = packed_inputs(LENGTHS, 8, 2, head_dim, dtype, seed=36)
+    scale = 1.0 / math.sqrt(head_dim)
+    out, lse = flash_attention_forward(q, k, v, cu, max(LENGTHS), scale)
+    want, want_lse = oracle_of(q, k, v, cu, max(LENGTHS), scale)
+    tol = TOLERANCE[dtype]
+    t.testing.assert_close(out.double().cpu(), t.from_numpy(want), rtol=tol, atol=tol)
+    t.testing.assert_close(lse.double().cpu(), t.from_numpy(want_lse), rtol=LSE_TOLERANCE, atol=LSE_TOLERANCE)
+
+
+@t.inference_mode()
 def test_prefill_rejects_unsupported_shapes_and_handles_empty():
-    q, k, v, cu = packed_inputs([5, 7], 4, 2, 12, t.bfloat16, seed=35)
+    q, k, v, cu = packed_inputs([5, 7], 4, 2, 520, t.bfloat16, seed=35)
     with pytest.raises(ValueError):
-        flash_attention_forward(q, k, v, cu, 7, 0.3)                  # head size not a multiple of 8
+        flash_attention_forward(q, k, v, cu, 7, 0.3)                  # head size above 512
     q, k, v, cu = packed_inputs([5, 7], 4, 2, 16, t.bfloat16, seed=35)
     with pytest.raises(ValueError):
         flash_attention_forward(q, k.float(), v, cu, 7, 0.3)          # mixed dtypes
