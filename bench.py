@@ -148,16 +148,18 @@ class _NoGC:
 
 
 def time_steps(setup: Setup, steps: int, warmup: int):
-    """Four timed regions of `steps` calls each, after `warmup` eager steps:
+    """Timed regions of `steps` calls each, after `warmup` eager steps:
       * graph replay of whole steps, LAYERS_PER_GRAPH steps per graph (no host work
         between steps, one graph launch per model step): ms per step, for the step as
         the two separate calls and as the fused call;
       * the split (decode) kernel alone, `steps` launches back to back on the
         current stream between two HIP events, pools rotating: its mean launch
-        duration, the figure the roofline divides by;
+        duration, the figure the roofline divides by; then the whole call (split and
+        combine) the same way, and the split's median with events around each launch;
       * eager steps with HIP events on the dispatch packet of every decode-kernel
         launch (hipExtLaunchKernel, here the fused kernel): per-dispatch kernel ms,
-        and eager ms per step.
+        and eager ms per step;
+      * eager steps as the reference runtime makes them, the two calls with no graph.
     """
     import ctypes
     import torch as t
@@ -237,9 +239,23 @@ def time_steps(setup: Setup, steps: int, warmup: int):
     launches = ctypes.c_int64(0)
     _native.check(lib.kvfp8_timing_read(ctypes.byref(total_ms), ctypes.byref(launches)), "kvfp8_timing_read")
     dispatch_ms = total_ms.value / max(1, launches.value)
+    # The drop-in under the reference's own runtime: eager steps as its two calls
+    # (append_kv, then decode_attention_wrapper; model/attention.py:88-99), no graph.
+    setup.fused = False
+    for i in range(warmup):
+        setup.step(i)
+    t.cuda.synchronize()
+    with _NoGC():
+        start.record()
+        for i in range(steps):
+            setup.step(warmup + i)
+        end.record()
+        t.cuda.synchronize()
+    eager_two_calls_ms = start.elapsed_time(end) / steps
+    setup.fused = fused
     return {"graph_ms": graph_ms, "separate_ms": separate_ms, "eager_ms": eager_ms, "split_ms": split_ms,
             "call_ms": call_ms, "split_median_ms": split_median_ms, "dispatch_ms": dispatch_ms,
-            "dispatch_launches": launches.value}
+            "dispatch_launches": launches.value, "eager_two_calls_ms": eager_two_calls_ms}
 
 
 def prefill_write(steps: int):
@@ -763,6 +779,7 @@ def measure(name: str, steps: int, warmup: int):
         "ms_per_step": ms,
         "separate_ms_per_step": times["separate_ms"],
         "eager_ms_per_step": eager_ms,
+        "eager_two_calls_ms_per_step": times["eager_two_calls_ms"],
         "split_kernel_ms": kernel_ms,
         "call_ms": times["call_ms"],
         "call_gbs": setup.decode_bytes / (times["call_ms"] * 1e-3) / 1e9,
@@ -779,7 +796,7 @@ def measure(name: str, steps: int, warmup: int):
     log(f"[{name}] B={s.batch} Hq={s.num_q_heads} Hkv={s.num_kv_heads} D={s.head_dim} tokens={s.total_tokens} "
         f"pools={setup.num_pools}x{setup.pool_bytes / 1e6:.0f}MB: {ms * 1e3:.1f} us/step (graph; "
         f"{times['separate_ms'] * 1e3:.1f} as two calls), "
-        f"{eager_ms * 1e3:.1f} us/step (eager), decode kernel {kernel_ms * 1e3:.1f} us back to back "
+        f"{eager_ms * 1e3:.1f} us/step (eager; {times['eager_two_calls_ms'] * 1e3:.1f} as two calls), decode kernel {kernel_ms * 1e3:.1f} us back to back "
         f"({result['kernel_gbs']:.0f} GB/s), split + combine {times['call_ms'] * 1e3:.1f} us "
         f"({result['call_gbs']:.0f} GB/s), {times['dispatch_ms'] * 1e3:.1f} us per-dispatch events, "
         f"step {result['gbs']:.0f} GB/s")
@@ -832,6 +849,7 @@ def main():
             "ms_per_step": round(r["ms_per_step"], 5),
             "separate_ms_per_step": round(r["separate_ms_per_step"], 5),
             "eager_ms_per_step": round(r["eager_ms_per_step"], 5),
+            "eager_two_calls_ms_per_step": round(r["eager_two_calls_ms_per_step"], 5),
             "decode_kernel_us": round(r["split_kernel_ms"] * 1e3, 2),
             "decode_kernel_gbs": round(r["kernel_gbs"], 1),
             "decode_kernel_frac": round(r["kernel_gbs"] / PEAK_HBM_GBS, 4),
@@ -882,6 +900,7 @@ def main():
         "ms_per_step": round(main_result["ms_per_step"], 5),
         "separate_ms_per_step": round(main_result["separate_ms_per_step"], 5),
         "eager_ms_per_step": round(main_result["eager_ms_per_step"], 5),
+        "eager_two_calls_ms_per_step": round(main_result["eager_two_calls_ms_per_step"], 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -896,7 +915,10 @@ def main():
             "timing": (f"steps replayed from HIP graphs of {LAYERS_PER_GRAPH} steps, the decode step of a "
                        f"{LAYERS_PER_GRAPH}-layer model (Llama-3-8B) with one attention step per layer, the layers "
                        f"cycling through {main_result['pools']} cache pools (together over twice the 256 MB "
-                       "last-level cache); separate_ms_per_step: the same step as the two calls append_kv + decode"),
+                       "last-level cache); separate_ms_per_step: the same step as the two calls append_kv + decode; "
+                       "eager_ms_per_step: the fused step launched eagerly, no graph; eager_two_calls_ms_per_step: "
+                       "the reference runtime's own pattern (model/attention.py:88-99), the two calls launched "
+                       "eagerly with no graph"),
             "pools_rotated": main_result["pools"],
             "pool_mb": round(main_result["pool_mb"], 1),
         },
