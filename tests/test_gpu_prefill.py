@@ -169,7 +169,7 @@ def test_config5_prefill_shape_against_float32_torch():
 
 
 @t.inference_mode()
-@pytest.mark.parametrize("dtype", [t.float32, t.bfloat16])
+@pytest.mark.parametrize("dtype", [t.float32, t.float16, t.bfloat16])
 @pytest.mark.parametrize("head_dim", [12, 20, 24, 96, 136, 192, 256, 300])
 def test_prefill_head_sizes_the_reference_takes(dtype, head_dim):
     """Head sizes beyond the matrix-core kernels' (not a multiple of 8, or above 128)
