@@ -9,11 +9,15 @@ graph and replayed gives the eager tokens and logits.
 
 from __future__ import annotations
 
+import dataclasses
+
 import pytest
 import torch as t
 
 from aiproj_amd.inference.greedy_decoder import GreedyDecoder
-from aiproj_amd.model.transformer import ModelConfig, TransformerLM
+from aiproj_amd.inference.page_allocator import PageAllocator
+from aiproj_amd.inference.paged_kv_cache import PagedKVCache
+from aiproj_amd.model.transformer import ModelConfig, StepMeta, TransformerLM
 from tests.helpers import FP8, FP8_MAX
 
 pytestmark = pytest.mark.gpu
@@ -43,6 +47,71 @@ def fake_quantized_caches(decoder):
             store(blocks, offsets, fake_quantize(ks), fake_quantize(vs))
 
         cache.append_kv = append_kv
+
+
+def _paged_model_run(model, rows, prompt_lengths, cache_dtype, block_size=16):
+    """Prefill rows[i][:prompt_lengths[i]] (packed, ragged) into fresh paged caches, then
+    feed each row's remaining tokens one decode step at a time (teacher forcing), the
+    sequences that are still running batched together. Returns {(row, position): logits}
+    for the prompt's last position and for every token fed to a decode step."""
+    cfg = model.cfg
+    max_len = max(len(r) for r in rows)
+    pages = len(rows) * (-(-max_len // block_size))
+    alloc = PageAllocator(pages, block_size, len(rows), max_len, "cuda")
+    caches = [PagedKVCache(pages, block_size, cfg.num_kv_heads, cfg.head_dim, "cuda", cache_dtype)
+              for _ in range(cfg.num_layers)]
+    slots = t.tensor([alloc.allocate_request(i, len(r)) for i, r in enumerate(rows)], device="cuda")
+    tokens = t.tensor([x for r, n in zip(rows, prompt_lengths) for x in r[:n]], device="cuda")
+    positions = t.cat([t.arange(n, device="cuda") for n in prompt_lengths])
+    cu = t.tensor([0] + list(t.tensor(prompt_lengths).cumsum(0).tolist()), dtype=t.int32, device="cuda")
+    ctx = alloc.create_container(slots, cu, positions)
+    logits = model(tokens, StepMeta("prefill", positions, ctx, cu_seqlens=cu, max_seqlen=max(prompt_lengths)), caches)
+    alloc.advance_batch(list(range(len(rows))), list(prompt_lengths))
+    out = {(i, n - 1): logits[i] for i, n in enumerate(prompt_lengths)}
+    for offset in range(max_len):
+        ids = [i for i, r in enumerate(rows) if prompt_lengths[i] + offset < len(r)]
+        if not ids:
+            break
+        pos = t.tensor([prompt_lengths[i] + offset for i in ids], device="cuda")
+        inputs = t.tensor([rows[i][prompt_lengths[i] + offset] for i in ids], device="cuda")
+        one_each = t.arange(len(ids) + 1, dtype=t.int32, device="cuda")
+        ctx = alloc.create_container(slots[ids], one_each, pos)
+        logits = model(inputs, StepMeta("decode", pos, ctx), caches)
+        alloc.advance_batch(ids, [1] * len(ids))
+        for k, i in enumerate(ids):
+            out[(i, prompt_lengths[i] + offset)] = logits[k]
+    return out
+
+
+@t.inference_mode()
+@pytest.mark.parametrize("dtype", [t.float16, t.bfloat16])
+def test_prefill_then_decode_matches_full_prefill(dtype):
+    """Reference tests/test_transformer_lm.py:29-65: a sequence split into a prefilled prompt
+    and decode steps through the paged cache gives, at every position, the logits of a
+    forward over the whole sequence up to that position (3e-2 as there for f16). The
+    whole-sequence forwards are one packed prefill of every prefix into a fresh cache.
+    Model and cache in f16 or bf16: the prefill kernel, the cache write and the decode
+    kernel must agree on positions (RoPE), pages and the history each step attends."""
+    # Weights ~ N(0, 0.08): scores of about unit scale, so attention is selective and a
+    # wrong position, page or history would move the logits (about unit scale too).
+    cfg = dataclasses.replace(SMALL, init_std=0.08)
+    g = t.Generator(device="cuda").manual_seed(12)
+    model = TransformerLM(cfg).to(device="cuda", dtype=dtype).init_weights(g).eval()
+    lengths, prompt_lengths = [37, 20, 9], [17, 2, 8]       # crosses page and tile edges
+    rows = [t.randint(0, cfg.vocab_size, (n,), generator=g, device="cuda").tolist() for n in lengths]
+    cached = _paged_model_run(model, rows, prompt_lengths, dtype)
+    keys = sorted(cached)
+    assert len(keys) == sum(lengths) - sum(prompt_lengths) + len(rows)
+    prefixes = [rows[i][:p + 1] for i, p in keys]
+    full = _paged_model_run(model, prefixes, [len(x) for x in prefixes], dtype)
+    # f16: the reference's 3e-2. bf16 carries 3 fewer mantissa bits, and at this weight
+    # scale the logits reach about 4, so its absolute bound is 0.1 (2.5% of that): two
+    # evaluation orders of the same attention, rounded through two bf16 layers. A wrong
+    # position, page or history moves logits by order 1.
+    atol = 3e-2 if dtype == t.float16 else 1e-1
+    for k, key in enumerate(keys):
+        t.testing.assert_close(cached[key].float(), full[(k, len(prefixes[k]) - 1)].float(), rtol=3e-2, atol=atol,
+                               msg=lambda m, key=key: f"row {key[0]} position {key[1]}: {m}")
 
 
 @t.inference_mode()
