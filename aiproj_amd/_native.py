@@ -165,8 +165,23 @@ def stream_handle(device: torch.device) -> int:
 
 
 def require_gpu(*tensors, what: str) -> torch.device:
-    """All tensors on one GPU device; the FP8 path has no CPU implementation."""
-    devices = {t.device for t in tensors if t is not None}
+    """All tensors on one GPU device; the FP8 path has no CPU implementation. The common
+    case compares device indices (get_device: -1 on the CPU) without building device
+    objects; any mismatch takes the descriptive path."""
+    first = None
+    index = None
+    for x in tensors:
+        if x is None:
+            continue
+        i = x.get_device()
+        if first is None:
+            first, index = x, i
+        elif i != index or (i < 0 and x.device != first.device):
+            index = None
+            break
+    if first is not None and index is not None and index >= 0 and first.is_cuda:
+        return first.device
+    devices = {x.device for x in tensors if x is not None}
     if len(devices) != 1:
         raise ValueError(f"{what}: tensors span devices {sorted(map(str, devices))}")
     device = devices.pop()

@@ -63,7 +63,7 @@ def _index_tensor(x: t.Tensor) -> t.Tensor:
 
 
 def decode_attention_wrapper(q, paged_kv_cache, cache_batch_context=None):
-    call = prepare_decode(q, paged_kv_cache, cache_batch_context)
+    call = prepare_decode(q, paged_kv_cache, cache_batch_context, _launch_now=True)
     if call.args is not None:
         call.run()
     return call.output
@@ -98,10 +98,33 @@ def _workspace_bytes(b, hq, hkv, d, bt_width, block_size, kv_code) -> int:
     return _native.lib().kvfp8_decode_workspace_bytes(b, hq, hkv, d, bt_width, block_size, kv_code)
 
 
-def prepare_decode(q, paged_kv_cache, cache_batch_context=None) -> DecodeCall:
+# Decode workspaces of the calls that launch at once (decode_attention_wrapper and the
+# fused step), one per (device, stream): such calls run in stream order, so each can
+# reuse the previous call's block (the workspace needs no initialization; every call
+# rewrites what it reads). A call that needs more gets a larger block. Prepared calls
+# (prepare_decode), which may be launched later and in halves, and every call under
+# graph capture take a block of their own, so no two of them share one.
+_WORKSPACES: dict = {}
+
+
+def _workspace(device: t.device, stream: int, nbytes: int) -> t.Tensor:
+    nbytes = max(nbytes, 1)
+    if t.cuda.is_current_stream_capturing():
+        return t.empty(nbytes, dtype=t.uint8, device=device)
+    key = (device.index, stream)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = t.empty(nbytes, dtype=t.uint8, device=device)
+        _WORKSPACES[key] = ws
+    return ws
+
+
+def prepare_decode(q, paged_kv_cache, cache_batch_context=None, _launch_now=False) -> DecodeCall:
     """Validate the arguments of `decode_attention_wrapper` (same forms, same
     asserts and errors), allocate its output and workspace, and return the
-    prepared call without launching anything."""
+    prepared call without launching anything. (`_launch_now`: the caller launches the
+    call right away on the current stream, so it may take the stream's shared
+    workspace.)"""
     if cache_batch_context is None:
         kv = paged_kv_cache                       # PagedKVRead form
         k_cache, v_cache = kv.k, kv.v
@@ -153,7 +176,11 @@ def prepare_decode(q, paged_kv_cache, cache_batch_context=None) -> DecodeCall:
 
     kv_code = _native.dtype_code(k_cache.dtype)
     ws_bytes = _workspace_bytes(b, hq, hkv, d, block_table.shape[1], block_size, kv_code)
-    workspace = t.empty(max(ws_bytes, 1), dtype=t.uint8, device=q.device)
+    stream = _native.stream_handle(device)
+    if _launch_now:
+        workspace = _workspace(device, stream, ws_bytes)
+    else:
+        workspace = t.empty(max(ws_bytes, 1), dtype=t.uint8, device=q.device)
 
     args = (
         q.data_ptr(), _native.dtype_code(q.dtype), q.stride(0), q.stride(1),
@@ -166,7 +193,7 @@ def prepare_decode(q, paged_kv_cache, cache_batch_context=None) -> DecodeCall:
         context_lengths.data_ptr(), _native.dtype_code(context_lengths.dtype),
         1.0 / math.sqrt(d),
         output.data_ptr(), workspace.data_ptr(), workspace.numel(),
-        _native.stream_handle(device),
+        stream,
     )
     keep = (q, k_cache, v_cache, k_scales, v_scales, block_table, cache_slots, context_lengths)
     return DecodeCall(output, workspace, args, keep)
@@ -216,7 +243,7 @@ def append_decode_attention(q, ks, vs, paged_kv_cache, cache_batch_context, refu
         cache.append_kv(blocks, offsets, ks, vs)
         return decode_attention_wrapper(q, cache, ctx)
     _native.require_gpu(ks, vs, cache.k, blocks, offsets, refused, what="append_decode_attention")
-    call = prepare_decode(q, cache, ctx)
+    call = prepare_decode(q, cache, ctx, _launch_now=True)
     if call.args is None:
         return call.output
     if vs.dtype != ks.dtype:
