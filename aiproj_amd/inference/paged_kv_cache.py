@@ -64,8 +64,12 @@ class PagedKVCache:
             raise ValueError("K/V and cache locations must describe the same packed tokens")
         if blocks.dtype not in (t.int32, t.int64) or offsets.dtype not in (t.int32, t.int64):
             raise ValueError("Cache locations must be integer tensors")
-        if any(x.device != self.k.device for x in (blocks, offsets, ks, vs)):
-            raise ValueError("K/V and cache locations must be on the cache device")
+        # Device indices first (get_device: no device objects); a CPU or meta cache, or
+        # any mismatch, takes the full comparison.
+        dev = self.k.get_device()
+        if dev < 0 or any(x.get_device() != dev for x in (blocks, offsets, ks, vs)):
+            if any(x.device != self.k.device for x in (blocks, offsets, ks, vs)):
+                raise ValueError("K/V and cache locations must be on the cache device")
 
         if self.quantized:
             quantize_append_wrapper(self, ks, vs, blocks, offsets)
