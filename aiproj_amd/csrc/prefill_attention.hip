@@ -616,6 +616,15 @@ prefill_fa_kernel(PrefillArgs a, int32_t units, int32_t upx, int32_t per_xcd) {
     const int gw = a.heads_per_block;
     const int64_t q_row = (int64_t)a.hq * kD * 2;         // bytes between tokens
     const int64_t kv_row = (int64_t)a.hkv * kD * 2;
+    // This lane's byte offset in a full K/V block: chunk slot c = lane + kFaThreads i
+    // holds row c / CPR, chunk (c % CPR) ^ (row % CPR) (below 64 kv_row < 2^32).
+    uint32_t chunk_off[CPT];
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+        const int c = threadIdx.x + kFaThreads * i;
+        const int row = c / CPR;
+        chunk_off[i] = (uint32_t)(row * kv_row + 16 * ((c % CPR) ^ (row % CPR)));
+    }
 
     // Asynchronous load of block kb of item it into LDS buffer `buf`. Keys past the
     // sequence read its last key (finite data, masked out of the scores).
@@ -627,7 +636,28 @@ prefill_fa_kernel(PrefillArgs a, int32_t units, int32_t upx, int32_t per_xcd) {
     // They set m0 (the LDS destination) themselves. The compiler reserves m0 and
     // writes it right before each instruction of its own that reads it, so it
     // holds no value across these statements (and a clobber list may not name it).
+    //
+    // A block whose 64 keys all lie inside the sequence is addressed as a wave-uniform
+    // base (scalar registers) plus this lane's fixed 32-bit offset (`chunk_off`, the
+    // same for every full block), so it costs no vector instructions. The sequence's
+    // last, partial block clamps each key to the sequence (per-lane 64-bit addresses).
     auto load_block = [&](const FaItem& it, int kb, int buf) __attribute__((always_inline)) {
+        if ((kb + 1) * kKeys <= it.L) {
+            const int64_t base = (int64_t)(it.s0 + kb * kKeys) * kv_row + (int64_t)it.hk * kD * 2;
+            const uint8_t* kb_base = a.k + base;
+            const uint8_t* vb_base = a.v + base;
+#pragma unroll
+            for (int i = 0; i < CPT; ++i) {
+                const uint32_t slot = (uint32_t)buf * (kKeys * ROW) + 16u * (uint32_t)(kFaThreads * i + 64 * wave);
+                __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+                                 :: "s"(__builtin_amdgcn_readfirstlane(k_lds0 + slot)), "v"(chunk_off[i]),
+                                    "s"(kb_base) : "memory");
+                __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+                                 :: "s"(__builtin_amdgcn_readfirstlane(v_lds0 + slot)), "v"(chunk_off[i]),
+                                    "s"(vb_base) : "memory");
+            }
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < CPT; ++i) {
             const int c = threadIdx.x + kFaThreads * i;         // slot written by this lane
@@ -790,10 +820,13 @@ prefill_fa_kernel(PrefillArgs a, int32_t units, int32_t upx, int32_t per_xcd) {
             if (__ballot(mx > m[qt] + 8.0f)) {
                 const float m_new = fmaxf(m[qt], max_across_rows(mx));
                 const float m_use = m_new == kNegInf ? 0.0f : m_new;
-                const float alpha = __builtin_amdgcn_exp2f(m[qt] - m_use);
-                l[qt] *= alpha;
+                // An item's first block finds the accumulators at zero: nothing to scale.
+                if (kb != 0) {
+                    const float alpha = __builtin_amdgcn_exp2f(m[qt] - m_use);
+                    l[qt] *= alpha;
 #pragma unroll
-                for (int nb = 0; nb < NB; ++nb) o[qt][nb] *= alpha;
+                    for (int nb = 0; nb < NB; ++nb) o[qt][nb] *= alpha;
+                }
                 m[qt] = m_new;
                 neg_m[qt] = -m_use;
             }
