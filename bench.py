@@ -156,9 +156,9 @@ def time_steps(setup: Setup, steps: int, warmup: int):
         current stream between two HIP events, pools rotating: its mean launch
         duration, the figure the roofline divides by; then the whole call (split and
         combine) the same way, and the split's median with events around each launch;
-      * eager steps with HIP events on the dispatch packet of every decode-kernel
-        launch (hipExtLaunchKernel, here the fused kernel): per-dispatch kernel ms,
-        and eager ms per step;
+      * eager steps (the fused call): ms per step; then the same steps with HIP events
+        on the dispatch packet of every decode-kernel launch (hipExtLaunchKernel, here
+        the fused kernel): per-dispatch kernel ms;
       * eager steps as the reference runtime makes them, the two calls with no graph.
     """
     import ctypes
@@ -226,8 +226,9 @@ def time_steps(setup: Setup, steps: int, warmup: int):
     split_median_ms = float(sorted(e0.elapsed_time(e1) for e0, e1 in pairs)[steps // 2])
     del calls, pairs
 
-    _native.check(lib.kvfp8_timing_enable(steps), "kvfp8_timing_enable")
-    t.cuda.synchronize()
+    # Eager steps (the fused call) with no instrumentation, then the same steps with
+    # HIP events on every decode-kernel dispatch (those events slow the eager loop, so
+    # they give only the per-dispatch kernel time).
     with _NoGC():
         start.record()
         for i in range(steps):
@@ -235,6 +236,12 @@ def time_steps(setup: Setup, steps: int, warmup: int):
         end.record()
         t.cuda.synchronize()
     eager_ms = start.elapsed_time(end) / steps
+    _native.check(lib.kvfp8_timing_enable(steps), "kvfp8_timing_enable")
+    t.cuda.synchronize()
+    with _NoGC():
+        for i in range(steps):
+            setup.step(warmup + i)
+        t.cuda.synchronize()
     total_ms = ctypes.c_double(0.0)
     launches = ctypes.c_int64(0)
     _native.check(lib.kvfp8_timing_read(ctypes.byref(total_ms), ctypes.byref(launches)), "kvfp8_timing_read")
